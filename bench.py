@@ -1,0 +1,307 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X W8A8 transformer-product path (one GPU).
+
+Headline (BASELINE.json `metric`): W8A8 GEMM TOPS and % of dense INT8 MFMA peak at
+M=4096, K=3072; DiT block linear ms.
+
+A step is BASELINE configs[1], the fused attention-input projection: an f16-valued
+hidden state [4096, 3072] (bf16 on the wire, as the reference's prepare_norm takes)
+-> prepare_norm_i8 (RMSNorm, group-256 Hadamard, per-token int8) -> gemm_i8 QKV with
+int8 W [9216, 3072] and per-channel scales -> f16 [4096, 9216]. `value` is that step's
+whole-job throughput in TOPS (2*M*N*K per step), inputs resident in HBM. Operand sets
+rotate through several copies so the 256 MB MALL cannot hold them between steps.
+
+Also reported: the north-star GEMM alone (M=4096, K=3072, N=12288), the per-block
+linear sequence of configs[3] (M=4544, 8 blocks) in ms per block, the dominant
+kernel's roofline (HIP events on the launch stream), and the CPU oracle timed on a
+bounded sample on this host (cpu_baseline).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "krea2-hrx_amd"))
+
+PEAK_INT8_TOPS = 5000.0  # MI355X dense INT8 MFMA, 5.0 POP/s
+PEAK_HBM_GBS = 8000.0
+METRIC = "W8A8 GEMM TOPS and % of INT8 MFMA peak at M=4096,K=3072; DiT block linear ms"
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-extra", action="store_true", help="headline step only")
+    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    return p.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested; the sharding design is in DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import krea2_w8a8 as k2
+
+    torch.cuda.set_device(0)
+    dev = "cuda"
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(2000)
+
+    M, K, N = 4096, 3072, 9216
+    pitch = k2.shape.gemm_pitch(K)
+
+    def hidden(rows, cols, seed):
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        x = torch.randn((rows, cols), generator=g, device=dev, dtype=torch.float32)
+        ch = torch.randperm(cols, generator=g, device=dev)[:8]
+        x[:, ch] *= 20.0
+        return x
+
+    def weights(rows, cols, seed):
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        w = torch.randint(-127, 128, (rows, cols), generator=g, device=dev, dtype=torch.int8)
+        s = torch.rand(rows, generator=g, device=dev) * 9e-3 + 1e-3
+        return w, s
+
+    # --- headline step: configs[1] -------------------------------------------------
+    copies = 4  # 4 x ~140 MB of operands > 256 MB MALL
+    sets = []
+    for c in range(copies):
+        h = hidden(M, K, 2100 + c).to(torch.float16).to(torch.bfloat16)  # f16 values, bf16 wire
+        w, ws = weights(N, pitch, 2200 + c)
+        sets.append(dict(
+            h=h,
+            ns=(torch.rand(K, generator=gen, device=dev) - 0.5),  # w - 1, w ~ U(0.5, 1.5)
+            zero=torch.zeros(K, device=dev),
+            q=torch.empty((M, pitch), dtype=torch.int8, device=dev),
+            s=torch.empty(M, dtype=torch.float32, device=dev),
+            w=w, ws=ws,
+            out=torch.empty((M, N), dtype=torch.float16, device=dev),
+        ))
+    cfg = k2.GemmConfig(k_size=K, n_size=N, k_stride=pitch, m_group=k2.shape.gemm_m_group())
+    stream = torch.cuda.current_stream()
+
+    def step(i, ev=None):
+        d = sets[i % copies]
+        if ev is not None:
+            ev[0].record(stream)
+        k2.prepare_norm_i8(d["h"], d["ns"], d["zero"], d["zero"], d["q"], d["s"], width=K,
+                           out_stride=pitch, eps=1e-6)
+        if ev is not None:
+            ev[1].record(stream)
+        k2.gemm_i8(d["q"], d["w"], d["ws"], d["s"], d["out"], cfg=cfg)
+        if ev is not None:
+            ev[2].record(stream)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    ops_step = 2.0 * M * N * K
+    value = ops_step / (ms_per_step * 1e-3) / 1e12
+
+    # Per-kernel durations: HIP events on the launch stream over a second timed pass.
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    for i in range(args.steps):
+        step(i, evs[i])
+    torch.cuda.synchronize()
+    prep_us = sum(e[0].elapsed_time(e[1]) for e in evs) * 1e3 / args.steps
+    gemm_us = sum(e[1].elapsed_time(e[2]) for e in evs) * 1e3 / args.steps
+    gemm_tops = ops_step / (gemm_us * 1e-6) / 1e12
+    prep_bytes = 2 * M * K + M * K + 4 * M + 4 * K
+    gemm_bytes = M * K + N * K + 4 * N + 4 * M + 2 * M * N
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded N(0,1) activations with 8 outlier channels x20, int8 U[-127,127] weights)",
+        "config": {
+            "workload": "configs[1] fused attention-input projection: prepare_norm_i8 -> gemm_i8 (QKV)",
+            "M": M, "K": K, "N": N, "k_stride": pitch, "eps": 1e-6,
+            "ops_per_step": ops_step,
+            "pct_of_int8_peak": round(100.0 * value / PEAK_INT8_TOPS, 2),
+        },
+        "kernels": {
+            "prepare_norm_i8_us": round(prep_us, 2),
+            "prepare_norm_i8_GBps": round(prep_bytes / (prep_us * 1e-6) / 1e9, 1),
+            "gemm_i8_us": round(gemm_us, 2),
+            "gemm_i8_TOPS": round(gemm_tops, 1),
+        },
+        "roofline": {
+            "kernel": "gemm_i8 (QKV, M=4096 K=3072 N=9216)",
+            "bound": "mfma",
+            "achieved": round(gemm_tops, 1),
+            "peak": PEAK_INT8_TOPS,
+            "unit": "TFLOP/s",
+            "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
+            "traffic": None,
+            "algorithmic_bytes": gemm_bytes,
+        },
+    }
+    del sets
+    torch.cuda.empty_cache()
+
+    if not args.no_extra:
+        result["north_star"] = north_star(k2, torch, weights, hidden, args)
+        torch.cuda.empty_cache()
+        result["block_linears"] = block_linears(k2, torch, weights, hidden, args)
+        torch.cuda.empty_cache()
+
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(M, K, N, pitch, args.cpu_seconds)
+
+    print(json.dumps(result), flush=True)
+
+
+def timed(torch, fn, steps, warmup):
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        fn(i)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def north_star(k2, torch, weights, hidden, args):
+    """The target GEMM alone: M=4096, K=3072, N=12288, plain epilogue."""
+    M, K, N = 4096, 3072, 12288
+    copies = 3
+    a = [torch.randint(-127, 128, (M, K), device="cuda", dtype=torch.int8) for _ in range(copies)]
+    s = [torch.rand(M, device="cuda") * 1e-2 + 1e-3 for _ in range(copies)]
+    ws = [weights(N, K, 3000 + c) for c in range(copies)]
+    out = [torch.empty((M, N), dtype=torch.float16, device="cuda") for _ in range(copies)]
+    cfg = k2.GemmConfig(k_size=K, n_size=N, k_stride=K)
+
+    def fn(i):
+        c = i % copies
+        k2.gemm_i8(a[c], ws[c][0], ws[c][1], s[c], out[c], cfg=cfg)
+
+    sec = timed(torch, fn, args.steps, args.warmup)
+    tops = 2.0 * M * N * K / sec / 1e12
+    return {"M": M, "K": K, "N": N, "us": round(sec * 1e6, 2), "TOPS": round(tops, 1),
+            "pct_of_int8_peak": round(100 * tops / PEAK_INT8_TOPS, 2), "target_pct": 60.0}
+
+
+def block_linears(k2, torch, weights, hidden, args):
+    """the per-block linear sequence of a 3072-hidden DiT, M=4544, 8 blocks.
+
+    Per block, in the reference's order (src/session/mod.rs:671-840, attention
+    excluded): prepare_norm -> QKV [9216x3072]; prepare_gated(attn, gate) -> out-proj
+    with residual [3072x3072]; prepare_norm -> SwiGLU up [2x12288x3072]; prepare_plain
+    -> down with residual [3072x12288]. Attention output and gate are synthetic.
+    """
+    M, H, I = 4544, 3072, 12288
+    blocks = 8
+    pitch_h, pitch_i = k2.shape.gemm_pitch(H), k2.shape.gemm_pitch(I)
+    x = hidden(M, H, 4000).to(torch.bfloat16)
+    attn = hidden(M, H, 4001).to(torch.float16)
+    gate = hidden(M, H, 4002).to(torch.float16)
+    ns = torch.rand(H, device="cuda") - 0.5
+    zero = torch.zeros(H, device="cuda")
+    one = torch.ones(H, device="cuda")
+    q = torch.empty((M, pitch_i), dtype=torch.int8, device="cuda")
+    qs = torch.empty(M, dtype=torch.float32, device="cuda")
+    qkv = torch.empty((M, 9216), dtype=torch.float16, device="cuda")
+    up = torch.empty((M, I), dtype=torch.float16, device="cuda")
+    wq, sq = weights(9216, pitch_h, 4100)
+    wo, so = weights(H, pitch_h, 4101)
+    wgu, sgu = weights(2 * I, pitch_h, 4102)
+    wd, sd = weights(H, pitch_i, 4103)
+    c_qkv = k2.GemmConfig(H, 9216, pitch_h)
+    c_o = k2.GemmConfig(H, H, pitch_h)
+    c_gu = k2.GemmConfig(H, 2 * I, pitch_h)
+    c_d = k2.GemmConfig(I, H, pitch_i, schedule_rows=int(k2.shape.gemm_schedule_rows(M)))
+
+    def block(_):
+        k2.prepare_norm_i8(x, ns, zero, zero, q, qs, width=H, out_stride=pitch_h, eps=1e-6)
+        k2.gemm_i8(q, wq, sq, qs, qkv, cfg=c_qkv)
+        k2.prepare_gated_i8(attn, gate, q, qs, width=H, out_stride=pitch_h, gate_stride=H)
+        k2.gemm_i8_resid(q, wo, so, qs, x, one, cfg=c_o)
+        k2.prepare_norm_i8(x, ns, zero, zero, q, qs, width=H, out_stride=pitch_h, eps=1e-6)
+        k2.gemm_i8_swiglu(q, wgu, sgu, qs, up, cfg=c_gu)
+        k2.prepare_plain_i8(up, q, qs, width=I, out_stride=pitch_i)
+        k2.gemm_i8_resid_256x256(q, wd, sd, qs, x, one, cfg=c_d)
+
+    def fn(i):
+        for _ in range(blocks):
+            block(i)
+
+    steps = max(2, args.steps // 8)
+    sec = timed(torch, fn, steps, max(1, args.warmup // 4))
+    ops_block = 2.0 * M * H * (9216 + H + 2 * I) + 2.0 * M * I * H
+    ms_block = sec * 1e3 / blocks
+    return {"M": M, "hidden": H, "intermediate": I, "blocks": blocks,
+            "ms_per_block": round(ms_block, 4),
+            "TOPS": round(ops_block / (ms_block * 1e-3) / 1e12, 1),
+            "ideal_ms_per_block_at_peak": round(ops_block / (PEAK_INT8_TOPS * 1e12) * 1e3, 4)}
+
+
+def cpu_baseline(M, K, N, pitch, budget_s):
+    """The CPU oracle (same arithmetic, OpenMP over tokens and N blocks) on a bounded
+    sample of the step: the first S tokens through prepare_norm + GEMM + epilogue."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle
+
+    threads = oracle.max_threads()
+    rng = np.random.default_rng(2100)
+    w = rng.integers(-127, 128, (N, pitch), dtype=np.int8)
+    ws = rng.uniform(1e-3, 1e-2, N).astype(np.float32)
+    ns = (rng.uniform(0.5, 1.5, K) - 1.0).astype(np.float32)
+    z = np.zeros(K, np.float32)
+
+    def run(rows):
+        x = rng.standard_normal((rows, K)).astype(np.float32)
+        u = x.astype(np.float16).astype(np.float32).view(np.uint32).astype(np.uint64)
+        h = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+        t0 = time.perf_counter()
+        q, s = oracle.prepare_norm(h, ns, z, z, K, pitch, 1e-6, threads=threads)
+        oracle.gemm_i8(q, w, rows, N, K, pitch, ws, s, threads=threads)
+        return time.perf_counter() - t0
+
+    rows = 8
+    t = run(rows)
+    rows = int(max(8, min(M, rows * budget_s / max(t, 1e-3))))
+    t = run(rows)
+    tops = 2.0 * rows * N * K / t / 1e12
+    return {"value": round(tops, 5), "unit": "TOPS", "cores": threads, "kind": "port",
+            "sample": f"first {rows} of {M} tokens through prepare_norm_i8 + gemm_i8 "
+                      f"(K={K}, N={N}) in {t:.1f} s", "seconds": round(t, 2)}
+
+
+if __name__ == "__main__":
+    main()

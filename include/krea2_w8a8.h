@@ -1,0 +1,175 @@
+/*
+ * krea2_w8a8.h -- the C ABI of the MI355X (gfx950) W8A8 transformer-product path.
+ *
+ * One entry point per reference kernel, with the reference's positional buffer
+ * bindings in the reference's order, its compile-time configuration passed as a
+ * struct (one field per `config.decl`), and its one runtime scalar (`tokens` or
+ * `m_size`). Every pointer is device memory the caller owns; the library never
+ * allocates. `stream` is a hipStream_t (NULL: the null stream). Calls enqueue
+ * work and return; they do not synchronise.
+ *
+ * Data types on the buffers:
+ *   f16 / bf16 activations: 16-bit IEEE half / bfloat16 bit patterns
+ *   int8 operands: row-major [rows][stride] bytes, K contiguous
+ *   scales, norm/modulation vectors, residual gates: float32
+ *
+ * Return codes preserve the reference's three-way error split
+ * (src/error.rs:11-29): caller-correctable arguments, host-side contract
+ * violations, and runtime (HIP) failures. k2w8_last_error() names the problem.
+ */
+#ifndef KREA2_W8A8_H
+#define KREA2_W8A8_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define K2W8_OK 0
+#define K2W8_INVALID_ARGUMENT (-1) /* Error::InvalidArgument */
+#define K2W8_INTERNAL (-2)         /* Error::Internal */
+#define K2W8_RUNTIME (-3)          /* Error::Runtime (a hipError_t) */
+
+/* The ABI revision this header describes. */
+#define K2W8_ABI_VERSION 1
+int k2w8_abi_version(void);
+
+/* Message of the last failure on the calling thread ("" after success). */
+const char *k2w8_last_error(void);
+
+/* kernels/prepare_norm_i8.loom:11-16 (width, out_stride, eps). */
+typedef struct k2w8_prepare_norm_cfg {
+  int64_t width;      /* K; multiple of 256, 256..32768 */
+  int64_t out_stride; /* q row pitch in bytes; multiple of 64, >= width */
+  float eps;
+} k2w8_prepare_norm_cfg;
+
+/* kernels/prepare_plain_i8.loom:10-13 (width, out_stride). */
+typedef struct k2w8_prepare_plain_cfg {
+  int64_t width;
+  int64_t out_stride;
+} k2w8_prepare_plain_cfg;
+
+/* kernels/prepare_gated_i8.loom:11-16 (width, out_stride, gate_stride). */
+typedef struct k2w8_prepare_gated_cfg {
+  int64_t width;
+  int64_t out_stride;
+  int64_t gate_stride; /* gate row pitch in elements; multiple of 8, >= width */
+} k2w8_prepare_gated_cfg;
+
+/* kernels/gemm_i8_256.loom:14-22 (k_size, n_size, k_stride, m_group), plus
+ * kernels/gemm_i8_resid_256x256.loom:26-27 (schedule_rows). m_group and
+ * schedule_rows are scheduling hints: they never change results. */
+typedef struct k2w8_gemm_cfg {
+  int64_t k_size;   /* K; multiple of 128, 128..65536 */
+  int64_t n_size;   /* N; multiple of 128, 128..32768 (SwiGLU: 2 x outputs) */
+  int64_t k_stride; /* operand row pitch in bytes; multiple of 64, >= k_size */
+  int64_t m_group;  /* m-tiles per raster group, 1..4 */
+  int64_t schedule_rows;
+} k2w8_gemm_cfg;
+
+/*
+ * prepare_norm: replaces krea2_prepare_norm_i8 (kernels/prepare_norm_i8.loom:18-22),
+ * bound by Session::block (src/session/mod.rs:682-700).
+ *   h          bf16 [tokens][width]
+ *   norm_scale f32 [width]  (applied as 1 + norm_scale)
+ *   mod_scale  f32 [width]  (applied as 1 + mod_scale)
+ *   mod_shift  f32 [width]
+ *   q          int8 [tokens][out_stride] (bytes >= width untouched)
+ *   q_scale    f32 [tokens]
+ */
+int k2w8_prepare_norm_i8(void *stream, const k2w8_prepare_norm_cfg *cfg, int64_t tokens,
+                         const void *h, const float *norm_scale, const float *mod_scale,
+                         const float *mod_shift, int8_t *q, float *q_scale);
+
+/*
+ * prepare_plain: replaces krea2_prepare_plain_i8 (kernels/prepare_plain_i8.loom:15-19),
+ * bound by Session::block (src/session/mod.rs:815-826) and Quantized::forward
+ * (src/training/quantized.rs:71-80).
+ *   h f16 [tokens][width] -> q int8 [tokens][out_stride], q_scale f32 [tokens]
+ */
+int k2w8_prepare_plain_i8(void *stream, const k2w8_prepare_plain_cfg *cfg, int64_t tokens,
+                          const void *h, int8_t *q, float *q_scale);
+
+/*
+ * prepare_gated: replaces krea2_prepare_gated_i8 (kernels/prepare_gated_i8.loom:18-22),
+ * bound by Session::block (src/session/mod.rs:757-770).
+ *   attn f16 [tokens][width], gate f16 [tokens][gate_stride]
+ *   -> q int8 [tokens][out_stride], q_scale f32 [tokens]
+ */
+int k2w8_prepare_gated_i8(void *stream, const k2w8_prepare_gated_cfg *cfg, int64_t tokens,
+                          const void *attn, const void *gate, int8_t *q, float *q_scale);
+
+/*
+ * gemm_i8: replaces krea2_gemm_i8_256 (kernels/gemm_i8_256.loom:24-36), bound by
+ * Session::gemm (src/session/mod.rs:650-669) and Quantized::forward
+ * (src/training/quantized.rs:81-101).
+ *   a       int8 [m][k_stride], w int8 [n_size][k_stride]
+ *   scale   f32 [n_size] (per output channel), a_scale f32 [m] (per token)
+ *   c       f16 [m][n_size] = f16(bf16((f32(acc) * scale[n]) * a_scale[m]))
+ */
+int k2w8_gemm_i8(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, const int8_t *a,
+                 const int8_t *w, const float *scale, const float *a_scale, void *c);
+
+/*
+ * gemm_i8_resid: replaces krea2_gemm_i8_resid_256 (kernels/gemm_i8_resid_256.loom:24-36).
+ *   c    bf16 [m][n_size], read and written in place:
+ *        c = bf16(c + bf16(gate[n] * bf16((f32(acc) * scale[n]) * a_scale[m])))
+ *   gate f32 [n_size]
+ */
+int k2w8_gemm_i8_resid(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, const int8_t *a,
+                       const int8_t *w, const float *scale, const float *a_scale, void *c,
+                       const float *gate);
+
+/* Replaces krea2_gemm_i8_resid_256x256 (kernels/gemm_i8_resid_256x256.loom), the
+ * down projection's kernel (src/kernels/shape.rs:68-90). Same bindings and
+ * results as k2w8_gemm_i8_resid. */
+int k2w8_gemm_i8_resid_256x256(void *stream, const k2w8_gemm_cfg *cfg, int64_t m,
+                               const int8_t *a, const int8_t *w, const float *scale,
+                               const float *a_scale, void *c, const float *gate);
+
+/*
+ * gemm_i8_swiglu: replaces krea2_gemm_i8_swiglu_256 (kernels/gemm_i8_swiglu_256.loom:24-36).
+ *   w rows interleaved in 16-row groups [gate o..o+15 | up o..o+15]
+ *   (src/checkpoint/plan.rs:193-208), scale likewise.
+ *   c f16 [m][n_size/2]: c[m][o] = f16(bf16(bf16(g*sigmoid(g)) * u)),
+ *   g = bf16((f32(acc[gc]) * scale[gc]) * a_scale[m]), gc = (o/16)*32 + o%16,
+ *   u likewise at gc + 16.
+ */
+int k2w8_gemm_i8_swiglu(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, const int8_t *a,
+                        const int8_t *w, const float *scale, const float *a_scale, void *c);
+
+/*
+ * gemm_i8_bias: no reference counterpart (the reference's W8A8 GEMMs carry no
+ * bias); the plain GEMM with an f16 bias added before the bf16 boundary:
+ *   c = f16(bf16((f32(acc) * scale[n]) * a_scale[m] + bias[n]))
+ */
+int k2w8_gemm_i8_bias(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, const int8_t *a,
+                      const int8_t *w, const float *scale, const float *a_scale,
+                      const void *bias, void *c);
+
+/*
+ * gemm_i8_acc: no reference counterpart; the exact int32 accumulators
+ * acc[m][n] = sum_{k < k_size} a[m][k] * w[n][k] with no epilogue. These are the
+ * partial sums a K-sharded (row-parallel) projection exchanges before its
+ * epilogue: integer addition is associative, so the exchange stays bit-exact.
+ *   acc int32 [m][n_size]
+ */
+int k2w8_gemm_i8_acc(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, const int8_t *a,
+                     const int8_t *w, int32_t *acc);
+
+/* Launch-shape rules of src/kernels/shape.rs:7-112. */
+int64_t k2w8_shape_gemm_pitch(int64_t k);    /* shape.rs:105-107 */
+int64_t k2w8_shape_capacity(int64_t tokens); /* shape.rs:12-16 */
+int64_t k2w8_shape_gemm_grid_rows(int64_t tokens); /* shape.rs:110-112 */
+int k2w8_shape_gemm_schedule_rows(int64_t tokens); /* shape.rs:97-99 */
+int64_t k2w8_shape_gemm_rows(void);    /* GEMM_ROWS, shape.rs:36 */
+int64_t k2w8_shape_gemm_m_group(void); /* GEMM_M_GROUP, shape.rs:93 */
+int64_t k2w8_shape_tokens_min(void);   /* TOKENS, shape.rs:8 */
+int64_t k2w8_shape_tokens_max(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,72 @@
+// Device-side scalar numerics of the W8A8 path: the rounding points and the
+// sigmoid's exponential. Every function is a fixed sequence of IEEE f32
+// operations; the library is compiled with -ffp-contract=off so nothing fuses.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace k2w8 {
+
+// f32 -> bf16 -> f32, round to nearest even on the bit pattern
+// (the rounding of src/numerics.rs:18-26 for finite values and infinities).
+__device__ __forceinline__ float bf16_round(float x) {
+  uint32_t u = __float_as_uint(x);
+  u = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;
+  return __uint_as_float(u);
+}
+
+__device__ __forceinline__ uint16_t bf16_bits(float x) {
+  uint32_t u = __float_as_uint(x);
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+__device__ __forceinline__ float bf16_value(uint16_t b) {
+  return __uint_as_float((uint32_t)b << 16);
+}
+
+// f32 -> f16 (hardware conversion, round to nearest even) and back.
+__device__ __forceinline__ uint16_t f16_bits(float x) {
+  _Float16 h = (_Float16)x;
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ float f16_value(uint16_t b) {
+  return (float)__builtin_bit_cast(_Float16, b);
+}
+
+__device__ __forceinline__ float f16_round(float x) { return (float)(_Float16)x; }
+
+// exp(x) for the sigmoids of the gated prepare and the SwiGLU epilogue:
+// Cody-Waite reduction x = n*ln2 + r (two-part ln2), e^r = 1 + r + r^2 q(r) with a
+// degree-4 least-squares q, then 2^n as two exact power-of-two factors. The CPU
+// oracle evaluates the identical operation sequence.
+__device__ __forceinline__ float sigmoid_exp(float x) {
+  if (x != x) return x;
+  if (x > 0x1.62e42ep+6f) return __builtin_inff();
+  if (x < -0x1.9fe368p+6f) return 0.0f;
+  float n = __builtin_rintf(x * 0x1.715476p+0f);
+  float r = __builtin_fmaf(n, -0x1.62e4p-1f, x);
+  r = __builtin_fmaf(n, -0x1.7f7d1cp-20f, r);
+  float q = __builtin_fmaf(0x1.6d4854p-10f, r, 0x1.121286p-7f);
+  q = __builtin_fmaf(q, r, 0x1.5554e6p-5f);
+  q = __builtin_fmaf(q, r, 0x1.5554d6p-3f);
+  q = __builtin_fmaf(q, r, 0.5f);
+  float r2 = r * r;
+  float p = 1.0f + __builtin_fmaf(q, r2, r);
+  int ni = (int)n;
+  int n1 = ni / 2;
+  int n2 = ni - n1;
+  float s1 = __uint_as_float((uint32_t)(n1 + 127) << 23);
+  float s2 = __uint_as_float((uint32_t)(n2 + 127) << 23);
+  return (p * s1) * s2;
+}
+
+// 1 / (1 + exp(-g)), correctly rounded division.
+__device__ __forceinline__ float sigmoid(float g) {
+  float e = sigmoid_exp(0.0f - g);
+  float den = 1.0f + e;
+  return 1.0f / den;
+}
+
+}  // namespace k2w8

@@ -1,0 +1,132 @@
+"""Loading ``libkrea2_w8a8.so`` and declaring its C ABI for ctypes.
+
+The library lives next to this package (``krea2-hrx_amd/libkrea2_w8a8.so``) and is
+built by ``krea2-hrx_amd/Makefile``. A missing library is an error: the W8A8 path
+has no CPU or PyTorch fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+library_path = os.path.join(os.path.dirname(_HERE), "libkrea2_w8a8.so")
+
+K2W8_OK = 0
+K2W8_INVALID_ARGUMENT = -1
+K2W8_INTERNAL = -2
+K2W8_RUNTIME = -3
+
+
+class Krea2Error(RuntimeError):
+    """A failed W8A8 call (the reference's ``krea2::Error``)."""
+
+
+class InvalidArgument(Krea2Error, ValueError):
+    """The request cannot be served as asked (``Error::InvalidArgument``)."""
+
+
+class Internal(Krea2Error):
+    """The host broke its own contract with a kernel (``Error::Internal``)."""
+
+
+class Runtime(Krea2Error):
+    """The GPU runtime failed or refused the work (``Error::Runtime``)."""
+
+
+class PrepareNormCfg(ctypes.Structure):
+    _fields_ = [("width", ctypes.c_int64), ("out_stride", ctypes.c_int64), ("eps", ctypes.c_float)]
+
+
+class PreparePlainCfg(ctypes.Structure):
+    _fields_ = [("width", ctypes.c_int64), ("out_stride", ctypes.c_int64)]
+
+
+class PrepareGatedCfg(ctypes.Structure):
+    _fields_ = [
+        ("width", ctypes.c_int64),
+        ("out_stride", ctypes.c_int64),
+        ("gate_stride", ctypes.c_int64),
+    ]
+
+
+class GemmCfg(ctypes.Structure):
+    _fields_ = [
+        ("k_size", ctypes.c_int64),
+        ("n_size", ctypes.c_int64),
+        ("k_stride", ctypes.c_int64),
+        ("m_group", ctypes.c_int64),
+        ("schedule_rows", ctypes.c_int64),
+    ]
+
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+
+# name -> (restype, argtypes); the exported surface of include/krea2_w8a8.h
+SIGNATURES = {
+    "k2w8_abi_version": (ctypes.c_int, []),
+    "k2w8_last_error": (ctypes.c_char_p, []),
+    "k2w8_prepare_norm_i8": (
+        ctypes.c_int,
+        [_P, ctypes.POINTER(PrepareNormCfg), _I64, _P, _P, _P, _P, _P, _P],
+    ),
+    "k2w8_prepare_plain_i8": (ctypes.c_int, [_P, ctypes.POINTER(PreparePlainCfg), _I64, _P, _P, _P]),
+    "k2w8_prepare_gated_i8": (
+        ctypes.c_int,
+        [_P, ctypes.POINTER(PrepareGatedCfg), _I64, _P, _P, _P, _P],
+    ),
+    "k2w8_gemm_i8": (ctypes.c_int, [_P, ctypes.POINTER(GemmCfg), _I64, _P, _P, _P, _P, _P]),
+    "k2w8_gemm_i8_resid": (ctypes.c_int, [_P, ctypes.POINTER(GemmCfg), _I64, _P, _P, _P, _P, _P, _P]),
+    "k2w8_gemm_i8_resid_256x256": (
+        ctypes.c_int,
+        [_P, ctypes.POINTER(GemmCfg), _I64, _P, _P, _P, _P, _P, _P],
+    ),
+    "k2w8_gemm_i8_swiglu": (ctypes.c_int, [_P, ctypes.POINTER(GemmCfg), _I64, _P, _P, _P, _P, _P]),
+    "k2w8_gemm_i8_bias": (ctypes.c_int, [_P, ctypes.POINTER(GemmCfg), _I64, _P, _P, _P, _P, _P, _P]),
+    "k2w8_gemm_i8_acc": (ctypes.c_int, [_P, ctypes.POINTER(GemmCfg), _I64, _P, _P, _P]),
+    "k2w8_shape_gemm_pitch": (_I64, [_I64]),
+    "k2w8_shape_capacity": (_I64, [_I64]),
+    "k2w8_shape_gemm_grid_rows": (_I64, [_I64]),
+    "k2w8_shape_gemm_schedule_rows": (ctypes.c_int, [_I64]),
+    "k2w8_shape_gemm_rows": (_I64, []),
+    "k2w8_shape_gemm_m_group": (_I64, []),
+    "k2w8_shape_tokens_min": (_I64, []),
+    "k2w8_shape_tokens_max": (_I64, []),
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library (loaded once). Raises ``Runtime`` if it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(library_path):
+            raise Runtime(
+                f"{library_path} is not built; run `make -C krea2-hrx_amd` "
+                "(or __graft_entry__.build())"
+            )
+        # torch first: the HIP runtime it loads is the one this library binds to.
+        import torch  # noqa: F401
+
+        handle = ctypes.CDLL(library_path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def check(code: int) -> None:
+    """Raise the error class matching a C ABI return code."""
+    if code == K2W8_OK:
+        return
+    message = lib().k2w8_last_error().decode(errors="replace")
+    if code == K2W8_INVALID_ARGUMENT:
+        raise InvalidArgument(message)
+    if code == K2W8_INTERNAL:
+        raise Internal(message)
+    raise Runtime(message)

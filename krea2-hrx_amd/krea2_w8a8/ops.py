@@ -1,0 +1,182 @@
+"""One call per reference kernel, with the reference's bindings and configuration.
+
+Binding order follows the Loom ``launch(...)`` signatures:
+  prepare_norm(h, norm_scale, mod_scale, mod_shift, q, q_scale)   kernels/prepare_norm_i8.loom:22
+  prepare_plain(h, q, q_scale)                                    kernels/prepare_plain_i8.loom:19
+  prepare_gated(attn, gate, q, q_scale)                           kernels/prepare_gated_i8.loom:22
+  gemm_i8*(a, w, scale, a_scale, c[, gate])                       kernels/gemm_i8_256.loom:36,
+                                                                  kernels/gemm_i8_resid_256.loom:36
+Configuration keys are the ``config.decl`` names. The runtime scalar (``tokens``
+or ``m``) defaults to the leading dimension of the first operand.
+
+Buffer extents are checked here, before the C ABI, because the ABI takes plain
+pointers; a short buffer is an ``InvalidArgument``, as in the reference.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from ._lib import (
+    GemmCfg,
+    InvalidArgument,
+    PrepareGatedCfg,
+    PrepareNormCfg,
+    PreparePlainCfg,
+    check,
+    lib,
+)
+
+
+def _stream(stream) -> ctypes.c_void_p:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def _buf(t: torch.Tensor, name: str, dtype, min_elems: int) -> ctypes.c_void_p:
+    if not isinstance(t, torch.Tensor):
+        raise InvalidArgument(f"{name} must be a tensor")
+    if t.device.type != "cuda":
+        raise InvalidArgument(f"{name} must be device memory, got {t.device}")
+    if dtype is not None and t.dtype != dtype:
+        raise InvalidArgument(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise InvalidArgument(f"{name} must be contiguous")
+    if t.numel() < min_elems:
+        raise InvalidArgument(f"{name} holds {t.numel()} elements, needs {min_elems}")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _tokens(t: torch.Tensor, tokens):
+    return int(t.shape[0]) if tokens is None else int(tokens)
+
+
+def prepare_norm_i8(h, norm_scale, mod_scale, mod_shift, q, q_scale, *, width, out_stride, eps,
+                    tokens=None, stream=None):
+    """Modulated RMSNorm, Hadamard rotation and per-token int8 quantisation.
+
+    ``h`` bf16 [tokens][width]; ``norm_scale``/``mod_scale``/``mod_shift`` f32 [width];
+    ``q`` int8 [tokens][out_stride]; ``q_scale`` f32 [tokens].
+    """
+    n = _tokens(h, tokens)
+    cfg = PrepareNormCfg(width, out_stride, eps)
+    args = (
+        _buf(h, "h", torch.bfloat16, n * width),
+        _buf(norm_scale, "norm_scale", torch.float32, width),
+        _buf(mod_scale, "mod_scale", torch.float32, width),
+        _buf(mod_shift, "mod_shift", torch.float32, width),
+        _buf(q, "q", torch.int8, (n - 1) * out_stride + width),
+        _buf(q_scale, "q_scale", torch.float32, n),
+    )
+    check(lib().k2w8_prepare_norm_i8(_stream(stream), ctypes.byref(cfg), n, *args))
+
+
+def prepare_plain_i8(h, q, q_scale, *, width, out_stride, tokens=None, stream=None):
+    """Hadamard rotation (f16 stages) and per-token int8 quantisation of f16 rows."""
+    n = _tokens(h, tokens)
+    cfg = PreparePlainCfg(width, out_stride)
+    args = (
+        _buf(h, "h", torch.float16, n * width),
+        _buf(q, "q", torch.int8, (n - 1) * out_stride + width),
+        _buf(q_scale, "q_scale", torch.float32, n),
+    )
+    check(lib().k2w8_prepare_plain_i8(_stream(stream), ctypes.byref(cfg), n, *args))
+
+
+def prepare_gated_i8(attn, gate, q, q_scale, *, width, out_stride, gate_stride, tokens=None,
+                     stream=None):
+    """attn x sigmoid(gate) (bf16 rounding points), rotation, per-token int8 quantisation."""
+    n = _tokens(attn, tokens)
+    cfg = PrepareGatedCfg(width, out_stride, gate_stride)
+    args = (
+        _buf(attn, "attn", torch.float16, n * width),
+        _buf(gate, "gate", torch.float16, (n - 1) * gate_stride + width),
+        _buf(q, "q", torch.int8, (n - 1) * out_stride + width),
+        _buf(q_scale, "q_scale", torch.float32, n),
+    )
+    check(lib().k2w8_prepare_gated_i8(_stream(stream), ctypes.byref(cfg), n, *args))
+
+
+@dataclass(frozen=True)
+class GemmConfig:
+    """The GEMM family's ``config.decl`` set (kernels/gemm_i8_256.loom:14-22)."""
+
+    k_size: int
+    n_size: int
+    k_stride: int
+    m_group: int = 4
+    schedule_rows: int = 0
+
+    def c(self) -> GemmCfg:
+        return GemmCfg(self.k_size, self.n_size, self.k_stride, self.m_group, self.schedule_rows)
+
+
+def _gemm_operands(cfg: GemmConfig, m: int, a, w, scale, a_scale):
+    return (
+        _buf(a, "a", torch.int8, (m - 1) * cfg.k_stride + cfg.k_size),
+        _buf(w, "w", torch.int8, (cfg.n_size - 1) * cfg.k_stride + cfg.k_size),
+        _buf(scale, "scale", torch.float32, cfg.n_size),
+        _buf(a_scale, "a_scale", torch.float32, m),
+    )
+
+
+def gemm_i8(a, w, scale, a_scale, c, *, cfg: GemmConfig, m=None, stream=None):
+    """c f16 [m][n] = f16(bf16((f32(a.w^T) * scale[n]) * a_scale[m]))."""
+    m = _tokens(a, m)
+    ops = _gemm_operands(cfg, m, a, w, scale, a_scale)
+    out = _buf(c, "c", torch.float16, m * cfg.n_size)
+    k = cfg.c()
+    check(lib().k2w8_gemm_i8(_stream(stream), ctypes.byref(k), m, *ops, out))
+
+
+def gemm_i8_resid(a, w, scale, a_scale, c, gate, *, cfg: GemmConfig, m=None, stream=None):
+    """In place on bf16 ``c`` [m][n]: c = bf16(c + bf16(gate[n] * bf16(dequantised acc)))."""
+    m = _tokens(a, m)
+    ops = _gemm_operands(cfg, m, a, w, scale, a_scale)
+    out = _buf(c, "c", torch.bfloat16, m * cfg.n_size)
+    g = _buf(gate, "gate", torch.float32, cfg.n_size)
+    k = cfg.c()
+    check(lib().k2w8_gemm_i8_resid(_stream(stream), ctypes.byref(k), m, *ops, out, g))
+
+
+def gemm_i8_resid_256x256(a, w, scale, a_scale, c, gate, *, cfg: GemmConfig, m=None, stream=None):
+    """The down projection's residual GEMM (same results as ``gemm_i8_resid``)."""
+    m = _tokens(a, m)
+    ops = _gemm_operands(cfg, m, a, w, scale, a_scale)
+    out = _buf(c, "c", torch.bfloat16, m * cfg.n_size)
+    g = _buf(gate, "gate", torch.float32, cfg.n_size)
+    k = cfg.c()
+    check(lib().k2w8_gemm_i8_resid_256x256(_stream(stream), ctypes.byref(k), m, *ops, out, g))
+
+
+def gemm_i8_swiglu(a, w, scale, a_scale, c, *, cfg: GemmConfig, m=None, stream=None):
+    """c f16 [m][n/2] = silu(gate) * up over 16-row interleaved gate|up weight rows."""
+    m = _tokens(a, m)
+    ops = _gemm_operands(cfg, m, a, w, scale, a_scale)
+    out = _buf(c, "c", torch.float16, m * (cfg.n_size // 2))
+    k = cfg.c()
+    check(lib().k2w8_gemm_i8_swiglu(_stream(stream), ctypes.byref(k), m, *ops, out))
+
+
+def gemm_i8_bias(a, w, scale, a_scale, bias, c, *, cfg: GemmConfig, m=None, stream=None):
+    """Plain GEMM with an f16 bias before the bf16 boundary (no reference counterpart)."""
+    m = _tokens(a, m)
+    ops = _gemm_operands(cfg, m, a, w, scale, a_scale)
+    b = _buf(bias, "bias", torch.float16, cfg.n_size)
+    out = _buf(c, "c", torch.float16, m * cfg.n_size)
+    k = cfg.c()
+    check(lib().k2w8_gemm_i8_bias(_stream(stream), ctypes.byref(k), m, *ops, b, out))
+
+
+def gemm_i8_acc(a, w, acc, *, cfg: GemmConfig, m=None, stream=None):
+    """acc int32 [m][n] = exact integer a.w^T, no epilogue (no reference counterpart)."""
+    m = _tokens(a, m)
+    pa = _buf(a, "a", torch.int8, (m - 1) * cfg.k_stride + cfg.k_size)
+    pw = _buf(w, "w", torch.int8, (cfg.n_size - 1) * cfg.k_stride + cfg.k_size)
+    out = _buf(acc, "acc", torch.int32, m * cfg.n_size)
+    k = cfg.c()
+    check(lib().k2w8_gemm_i8_acc(_stream(stream), ctypes.byref(k), m, pa, pw, out))
