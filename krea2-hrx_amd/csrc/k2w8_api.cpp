@@ -38,11 +38,17 @@ int runtime(const char *stage, hipError_t e) {
 int ensure_configured(const char *stage) {
   static std::once_flag once;
   static hipError_t status = hipSuccess;
+  static const char *what = "";
   std::call_once(once, [] {
+    what = "enabling the prepare kernels' LDS";
     status = k2w8::configure_prepare_lds();
-    if (status == hipSuccess) status = k2w8::configure_gemm_lds();
+    if (status == hipSuccess) {
+      what = "enabling the GEMM kernels' LDS";
+      status = k2w8::configure_gemm_lds();
+    }
   });
-  if (status != hipSuccess) return runtime(stage, status);
+  if (status != hipSuccess)
+    return fail(K2W8_RUNTIME, "%s: %s: %s", stage, what, hipGetErrorString(status));
   return K2W8_OK;
 }
 

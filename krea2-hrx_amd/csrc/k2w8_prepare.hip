@@ -277,7 +277,8 @@ hipError_t launch_prepare(int kind, hipStream_t stream, int64_t tokens, const Pr
 }
 
 hipError_t configure_prepare_lds() {
-  const int max_lds = 160 * 1024;
+  // The widest row, 32768 f32 values plus four floats of padding per 64.
+  const int max_lds = (32768 + (32768 >> 6) * 4) * (int)sizeof(float);
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(prepare_kernel<kNorm>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
   if (e != hipSuccess) return e;
