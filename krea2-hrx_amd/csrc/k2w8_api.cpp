@@ -98,8 +98,9 @@ int check_gemm(const char *stage, const k2w8_gemm_cfg *cfg, int64_t m, const int
       m * cfg->n_size >= (int64_t(1) << 31))
     return fail(K2W8_INVALID_ARGUMENT, "%s: operands exceed 2^31 elements", stage);
   if (!a || !w || !scale || !a_scale || !c) return fail(K2W8_INVALID_ARGUMENT, "%s: null buffer", stage);
-  if (!aligned(a, 16) || !aligned(w, 16) || !aligned(scale, 4) || !aligned(a_scale, 4) || !aligned(c, 4))
-    return fail(K2W8_INVALID_ARGUMENT, "%s: a and w must be 16-byte aligned", stage);
+  if (!aligned(a, 16) || !aligned(w, 16) || !aligned(scale, 16) || !aligned(c, 16) ||
+      !aligned(a_scale, 4))
+    return fail(K2W8_INVALID_ARGUMENT, "%s: a, w, scale and c must be 16-byte aligned", stage);
   return K2W8_OK;
 }
 
@@ -110,6 +111,8 @@ int run_gemm(const char *stage, int epi, void *stream, const k2w8_gemm_cfg *cfg,
   if (rc != K2W8_OK) return rc;
   if (epi == k2w8::kEpiResid && !gate) return fail(K2W8_INVALID_ARGUMENT, "%s: null gate", stage);
   if (epi == k2w8::kEpiBias && !bias) return fail(K2W8_INVALID_ARGUMENT, "%s: null bias", stage);
+  if ((gate && !aligned(gate, 16)) || (bias && !aligned(bias, 16)))
+    return fail(K2W8_INVALID_ARGUMENT, "%s: gate and bias must be 16-byte aligned", stage);
   if ((rc = ensure_configured(stage)) != K2W8_OK) return rc;
   k2w8::GemmLaunch l;
   l.a = a;

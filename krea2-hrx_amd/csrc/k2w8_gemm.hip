@@ -1,14 +1,15 @@
 // INT8 GEMM family of the W8A8 path for gfx950 (CDNA4):
 //   acc[m][n] = sum_k A[m][k] * W[n][k]   (exact int32, v_mfma_i32_32x32x32_i8)
 // followed by a fused dequantising epilogue (plain f16, bf16 gated residual in
-// place, SwiGLU, or plain + bias).
+// place, SwiGLU, plain + bias, or the raw int32 accumulators).
 //
 // Workgroup tile BM x BN with a 128-byte K step; both operands are K-contiguous
 // rows, staged through LDS in a 16-byte-chunk XOR swizzle and double buffered:
 // the next K step's global loads are in flight while the current step's MFMAs
-// run. Each wave64 owns a (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA blocks.
-// Workgroups are numbered XCD-major (consecutive tiles land on one XCD's L2),
-// then grouped m_group m-tiles per sweep of n.
+// run, and each wave reads the next 32-byte K slice's fragments from LDS while
+// the current slice's MFMAs issue. Each wave64 owns a (BM/WM) x (BN/WN) sub-tile
+// of 32x32 MFMA blocks. Workgroups are numbered XCD-major (consecutive tiles land
+// on one XCD's L2), then grouped m_group m-tiles per sweep of n.
 //
 // Reference: kernels/gemm_i8_256.loom (tile, raster groups :98-132, ghost rows
 // :169-216, epilogue :558-629), kernels/gemm_i8_resid_256.loom:607-635,
@@ -21,12 +22,11 @@
 
 namespace k2w8 {
 
-namespace {
+namespace gemm {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-constexpr int kBK = 128;  // bytes of K per stage
 constexpr int kXcds = 8;  // MI355X: 8 XCDs, workgroups dispatched round-robin
 
 struct GemmArgs {
@@ -38,73 +38,246 @@ struct GemmArgs {
   int m, n, k, lda, m_group;
 };
 
-// Byte offset of 16-byte chunk `c` (0..7) of staged row `r`: chunks of eight
-// consecutive rows are permuted so a column of chunks spans all banks.
-__device__ __forceinline__ int swz(int r, int c) { return (r << 7) | (((c ^ r) & 7) << 4); }
+#ifndef K2W8_SWZ_SHIFT
+#define K2W8_SWZ_SHIFT 1
+#endif
 
-template <int BM, int BN, int WM, int WN, int EPI>
+// Staged operand rows are BK bytes = BK/16 chunks of 16 bytes. The chunk index is
+// XORed with bits of the row so that the consecutive rows one LDS cycle serves (one
+// chunk each) land on distinct banks.
+template <int BK>
+__device__ __forceinline__ int swz_key(int r) {
+  return (r >> K2W8_SWZ_SHIFT) & (BK / 16 - 1);
+}
+
+// One 16-byte-per-lane global -> LDS transfer (global_load_lds_dwordx4): lane l
+// writes LDS bytes [lds + 16 l, lds + 16 l + 16) from global address base + voff.
+// Issued through asm so that the waits for it are placed by hand (the compiler
+// would otherwise wait for every transfer in flight before any LDS read).
+__device__ __forceinline__ void dma16(uint32_t lds, const int8_t *base, uint32_t voff) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds) : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Tile of workgroup `bid`: XCD-major renumbering, then m_group m-tiles per n sweep.
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int m_group, int &tm,
+                                        int &tn) {
+  const int total = tiles_m * tiles_n;
+  const int per_xcd = total / kXcds;
+  if (bid < per_xcd * kXcds) bid = (bid % kXcds) * per_xcd + bid / kXcds;
+  const int span = m_group * tiles_n;
+  const int group = bid / span, in_group = bid - group * span;
+  const int first_m = group * m_group;
+  const int rows_in_group = min(tiles_m - first_m, m_group);
+  tm = first_m + in_group % rows_in_group;
+  tn = in_group / rows_in_group;
+}
+
+// One BK-byte K step from an LDS stage: BK/32 slices of 32 bytes, the next slice's
+// fragments read while the current slice's MFMAs issue.
+template <int BK, int FM, int FN>
+__device__ __forceinline__ void mma_stage(v16i (&acc)[FM][FN], const uint8_t *stage,
+                                          const int (&a_row_off)[FM], const int (&b_row_off)[FN],
+                                          int kh, int rsw) {
+  v4i af[2][FM], bf[2][FN];
+  {
+    const int c = (kh ^ rsw) << 4;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) af[0][i] = *reinterpret_cast<const v4i *>(stage + a_row_off[i] + c);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) bf[0][j] = *reinterpret_cast<const v4i *>(stage + b_row_off[j] + c);
+  }
+#pragma unroll
+  for (int s = 0; s < BK / 32; ++s) {
+    const int cur = s & 1;
+    if (s + 1 < BK / 32) {
+      const int c = (((s + 1) * 2 + kh) ^ rsw) << 4;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        af[cur ^ 1][i] = *reinterpret_cast<const v4i *>(stage + a_row_off[i] + c);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bf[cur ^ 1][j] = *reinterpret_cast<const v4i *>(stage + b_row_off[j] + c);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[cur][j], af[cur][i], acc[i][j], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Epilogue of one wave's (32 FM) x (32 FN) sub-tile at rows m_base.., columns n_base..
+template <int EPI, int FM, int FN>
+__device__ __forceinline__ void store_tile(const GemmArgs &g, v16i (&acc)[FM][FN], int m_base,
+                                           int n_base, int fr, int kh) {
+  // The MFMAs run with the weights as their row operand, so block (i, j) holds C^T:
+  // lane (fr, kh) owns token m = m_base + 32i + fr and, in register e, channel
+  // n = n_base + 32j + 8(e/4) + 4kh + e%4. Each lane therefore holds
+  // four runs of four consecutive channels of one token: 8-byte f16 / bf16 stores.
+  int64_t m_row[FM];
+  float as[FM];
+  bool live[FM];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int m = m_base + i * 32 + fr;
+    live[i] = m < g.m;
+    m_row[i] = live[i] ? m : g.m - 1;
+    as[i] = (EPI == kEpiAcc) ? 1.0f : g.a_scale[m_row[i]];
+  }
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int nb = n_base + j * 32 + kh * 4;  // channel of register 0
+    if (EPI == kEpiSwiglu) {
+      // registers 0-7: gate channels 8q+4kh+r (q<2) of the 32-channel group,
+      // registers 8-15: the matching up channels, 16 further on
+      float4 wg[2], wu[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        wg[q] = *reinterpret_cast<const float4 *>(g.w_scale + nb + 8 * q);
+        wu[q] = *reinterpret_cast<const float4 *>(g.w_scale + nb + 16 + 8 * q);
+      }
+      const int ob = ((n_base + j * 32) >> 1) + kh * 4;  // output of register 0
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        if (!live[i]) continue;
+        uint16_t *out = static_cast<uint16_t *>(g.c) + m_row[i] * (g.n >> 1) + ob;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const float gs[4] = {wg[q].x, wg[q].y, wg[q].z, wg[q].w};
+          const float us[4] = {wu[q].x, wu[q].y, wu[q].z, wu[q].w};
+          uint32_t packed[2];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float gv = bf16_round(((float)acc[i][j][4 * q + r] * gs[r]) * as[i]);
+            const float uv = bf16_round(((float)acc[i][j][8 + 4 * q + r] * us[r]) * as[i]);
+            const float silu = bf16_round(gv * sigmoid(gv));
+            const uint32_t h = f16_bits(bf16_round(silu * uv));
+            if (r & 1) packed[r >> 1] |= h << 16; else packed[r >> 1] = h;
+          }
+          *reinterpret_cast<uint2 *>(out + 8 * q) = make_uint2(packed[0], packed[1]);
+        }
+      }
+      continue;
+    }
+    float ws[16], extra[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (EPI != kEpiAcc) {
+        const float4 v = *reinterpret_cast<const float4 *>(g.w_scale + nb + 8 * q);
+        ws[4 * q] = v.x; ws[4 * q + 1] = v.y; ws[4 * q + 2] = v.z; ws[4 * q + 3] = v.w;
+      }
+      if (EPI == kEpiResid) {
+        const float4 v = *reinterpret_cast<const float4 *>(g.gate + nb + 8 * q);
+        extra[4 * q] = v.x; extra[4 * q + 1] = v.y; extra[4 * q + 2] = v.z; extra[4 * q + 3] = v.w;
+      }
+      if (EPI == kEpiBias) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(g.bias + nb + 8 * q);
+        extra[4 * q] = f16_value(v.x & 0xffffu); extra[4 * q + 1] = f16_value(v.x >> 16);
+        extra[4 * q + 2] = f16_value(v.y & 0xffffu); extra[4 * q + 3] = f16_value(v.y >> 16);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      if (!live[i]) continue;
+      if (EPI == kEpiAcc) {
+        int32_t *out = static_cast<int32_t *>(g.c) + m_row[i] * g.n + nb;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<v4i *>(out + 8 * q) =
+              v4i{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        continue;
+      }
+      uint16_t *out = static_cast<uint16_t *>(g.c) + m_row[i] * g.n + nb;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint2 prior = make_uint2(0, 0);
+        if (EPI == kEpiResid) prior = *reinterpret_cast<const uint2 *>(out + 8 * q);
+        const uint32_t pw[2] = {prior.x, prior.y};
+        uint32_t packed[2];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int e = 4 * q + r;
+          const float v = ((float)acc[i][j][e] * ws[e]) * as[i];
+          uint32_t h;
+          if (EPI == kEpiPlain) {
+            h = f16_bits(bf16_round(v));
+          } else if (EPI == kEpiBias) {
+            h = f16_bits(bf16_round(v + extra[e]));
+          } else {  // residual: x = bf16(x + bf16(gate * bf16(v)))
+            const float gated = bf16_round(bf16_round(v) * extra[e]);
+            const float x = bf16_value((uint16_t)((r & 1) ? (pw[r >> 1] >> 16) : (pw[r >> 1] & 0xffffu)));
+            h = bf16_bits(x + gated);
+          }
+          if (r & 1) packed[r >> 1] |= h << 16; else packed[r >> 1] = h;
+        }
+        *reinterpret_cast<uint2 *>(out + 8 * q) = make_uint2(packed[0], packed[1]);
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int WM, int WN, int BK, int STAGES, int EPI>
 __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
-  constexpr int kThreads = WM * WN * 64;
+  constexpr int kWaves = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;  // wave sub-tile
   constexpr int FM = WTM / 32, FN = WTN / 32;  // 32x32 blocks per wave
-  constexpr int kAChunks = BM * (kBK / 16) / kThreads;
-  constexpr int kBChunks = BN * (kBK / 16) / kThreads;
-  constexpr int kStage = (BM + BN) * kBK;
-  static_assert(kAChunks * kThreads == BM * 8 && kBChunks * kThreads == BN * 8, "chunking");
+  constexpr int kCpr = BK / 16;                // 16-byte chunks per staged row
+  constexpr int kRowsPerKb = 1024 / BK;        // rows one transfer instruction fills
+  constexpr int kAIns = BM * BK / 1024 / kWaves;  // transfers per wave per stage
+  constexpr int kBIns = BN * BK / 1024 / kWaves;
+  constexpr int kStage = (BM + BN) * BK;
+  constexpr int kIns = kAIns + kBIns;
+  static_assert(kAIns * kWaves * 1024 == BM * BK && kBIns * kWaves * 1024 == BN * BK, "staging");
+  static_assert(BK % 32 == 0 && STAGES >= 2, "pipeline");
   extern __shared__ __align__(16) uint8_t smem[];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  // Tile of this workgroup.
-  const int tiles_m = (g.m + BM - 1) / BM, tiles_n = g.n / BN;
-  const int total = tiles_m * tiles_n;
-  int bid = blockIdx.x;
-  const int per_xcd = total / kXcds;
-  if (bid < per_xcd * kXcds) bid = (bid % kXcds) * per_xcd + bid / kXcds;
-  const int span = g.m_group * tiles_n;
-  const int group = bid / span, in_group = bid - group * span;
-  const int first_m = group * g.m_group;
-  const int rows_in_group = min(tiles_m - first_m, g.m_group);
-  const int tm = first_m + in_group % rows_in_group;
-  const int tn = in_group / rows_in_group;
+  int tm, tn;
+  tile_of(blockIdx.x, (g.m + BM - 1) / BM, g.n / BN, g.m_group, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
 
-  // Global -> LDS staging: chunk q = tid + i*kThreads is row q/8, 16-byte chunk q%8.
-  // Ghost rows past m read row m-1; their results are never stored.
-  uint32_t a_off[kAChunks], b_off[kBChunks];
-  int a_lds[kAChunks], b_lds[kBChunks];
+  // Transfers: wave w's instruction i fills 1 KiB block b = w*kAIns + i of the stage's
+  // A rows (then likewise B): rows b*kRowsPerKb + lane/kCpr, physical chunk lane%kCpr,
+  // which holds logical K chunk (lane%kCpr) ^ key(row). Ghost rows past m read row
+  // m-1; their results are never stored.
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
+  uint32_t a_off[kAIns], b_off[kBIns];
 #pragma unroll
-  for (int i = 0; i < kAChunks; ++i) {
-    int q = tid + i * kThreads, r = q >> 3, c = q & 7;
-    int gr = min(m0 + r, g.m - 1);
-    a_off[i] = (uint32_t)gr * (uint32_t)g.lda + (uint32_t)(c * 16);
-    a_lds[i] = swz(r, c);
+  for (int i = 0; i < kAIns; ++i) {
+    const int r = (wave * kAIns + i) * kRowsPerKb + lane / kCpr;
+    const int c = (lane % kCpr) ^ swz_key<BK>(r);
+    a_off[i] = (uint32_t)min(m0 + r, g.m - 1) * (uint32_t)g.lda + c * 16;
   }
 #pragma unroll
-  for (int i = 0; i < kBChunks; ++i) {
-    int q = tid + i * kThreads, r = q >> 3, c = q & 7;
-    b_off[i] = (uint32_t)(n0 + r) * (uint32_t)g.lda + (uint32_t)(c * 16);
-    b_lds[i] = BM * kBK + swz(r, c);
+  for (int i = 0; i < kBIns; ++i) {
+    const int r = (wave * kBIns + i) * kRowsPerKb + lane / kCpr;
+    const int c = (lane % kCpr) ^ swz_key<BK>(r);
+    b_off[i] = (uint32_t)(n0 + r) * (uint32_t)g.lda + c * 16;
   }
+  const uint32_t a_lds = lds0 + wave * kAIns * 1024;
+  const uint32_t b_lds = lds0 + BM * BK + wave * kBIns * 1024;
 
-  uint4 ra[kAChunks], rb[kBChunks];
-  auto load_global = [&](int kt) {
-    const uint32_t ko = (uint32_t)kt * kBK;
+  const int kt_count = g.k / BK;
+  auto issue = [&](int kt) {
+    const uint32_t so = (uint32_t)((kt % STAGES) * kStage), ko = (uint32_t)(kt * BK);
 #pragma unroll
-    for (int i = 0; i < kAChunks; ++i)
-      ra[i] = *reinterpret_cast<const uint4 *>(g.a + (a_off[i] + ko));
+    for (int i = 0; i < kAIns; ++i) dma16(a_lds + so + i * 1024, g.a, a_off[i] + ko);
 #pragma unroll
-    for (int i = 0; i < kBChunks; ++i)
-      rb[i] = *reinterpret_cast<const uint4 *>(g.w + (b_off[i] + ko));
+    for (int i = 0; i < kBIns; ++i) dma16(b_lds + so + i * 1024, g.w, b_off[i] + ko);
   };
-  auto store_lds = [&](int stage) {
-    uint8_t *base = smem + stage * kStage;
 #pragma unroll
-    for (int i = 0; i < kAChunks; ++i) *reinterpret_cast<uint4 *>(base + a_lds[i]) = ra[i];
-#pragma unroll
-    for (int i = 0; i < kBChunks; ++i) *reinterpret_cast<uint4 *>(base + b_lds[i]) = rb[i];
-  };
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < kt_count) issue(s);
 
   v16i acc[FM][FN];
 #pragma unroll
@@ -116,126 +289,70 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
 
   const int wm = wave / WN, wn = wave % WN;
   const int fr = lane & 31, kh = lane >> 5;
-  const int kt_count = g.k / kBK;
-
-  load_global(0);
-  store_lds(0);
-  __syncthreads();
+  // Per-lane LDS byte offsets of this wave's fragment rows (chunk added per K slice;
+  // a lane's fragment rows differ by multiples of 32 and share the swizzle key).
+  int a_row_off[FM], b_row_off[FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) a_row_off[i] = (wm * WTM + i * 32 + fr) * BK;
+#pragma unroll
+  for (int j = 0; j < FN; ++j) b_row_off[j] = BM * BK + (wn * WTN + j * 32 + fr) * BK;
+  const int rsw = swz_key<BK>(fr);
 
   for (int kt = 0; kt < kt_count; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < kt_count) load_global(kt + 1);
-    const uint8_t *sa = smem + cur * kStage;
-    const uint8_t *sb = sa + BM * kBK;
-#pragma unroll
-    for (int s = 0; s < kBK / 32; ++s) {
-      const int kc = 2 * s + kh;
-      v4i af[FM], bf[FN];
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-        af[i] = *reinterpret_cast<const v4i *>(sa + swz(wm * WTM + i * 32 + fr, kc));
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-        bf[j] = *reinterpret_cast<const v4i *>(sb + swz(wn * WTN + j * 32 + fr, kc));
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-    if (kt + 1 < kt_count) store_lds(cur ^ 1);
-    __syncthreads();
+    // This wave's transfers for step kt are done once at most the later stages'
+    // transfers are outstanding; the barrier then covers every wave's, and every
+    // wave's reads of the stage the next transfer overwrites.
+    if (kt + STAGES - 2 < kt_count)
+      wait_vmcnt<(STAGES - 2) * kIns>();
+    else
+      wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    if (kt + STAGES - 1 < kt_count) issue(kt + STAGES - 1);
+    mma_stage<BK, FM, FN>(acc, smem + (kt % STAGES) * kStage, a_row_off, b_row_off, kh, rsw);
   }
 
-  // Epilogue. Accumulator register e of block (i, j) holds row
-  // (e/4)*8 + kh*4 + e%4 and column fr of the block.
-#pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int n = n0 + wn * WTN + j * 32 + fr;
-    const float ws = (EPI == kEpiAcc) ? 1.0f : g.w_scale[n];
-    float gate_n = 0.0f, bias_n = 0.0f;
-    if (EPI == kEpiResid) gate_n = g.gate[n];
-    if (EPI == kEpiBias) bias_n = f16_value(g.bias[n]);
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int m = m0 + wm * WTM + i * 32 + (e >> 2) * 8 + kh * 4 + (e & 3);
-        const bool live = m < g.m;
-        const float as = (EPI == kEpiAcc) ? 1.0f : g.a_scale[live ? m : g.m - 1];
-        const float prod = (float)acc[i][j][e] * ws;
-        if (EPI == kEpiAcc) {
-          if (live) static_cast<int32_t *>(g.c)[(int64_t)m * g.n + n] = acc[i][j][e];
-        } else if (EPI == kEpiPlain) {
-          if (live)
-            static_cast<uint16_t *>(g.c)[(int64_t)m * g.n + n] = f16_bits(bf16_round(prod * as));
-        } else if (EPI == kEpiBias) {
-          if (live)
-            static_cast<uint16_t *>(g.c)[(int64_t)m * g.n + n] =
-                f16_bits(bf16_round(prod * as + bias_n));
-        } else if (EPI == kEpiResid) {
-          if (live) {
-            uint16_t *x = static_cast<uint16_t *>(g.c) + (int64_t)m * g.n + n;
-            float lin = bf16_round(prod * as);
-            float gated = bf16_round(lin * gate_n);
-            float prior = bf16_value(*x);
-            *x = bf16_bits(prior + gated);
-          }
-        } else {  // SwiGLU: columns fr < 16 are gates, fr >= 16 the matching ups
-          const float v = bf16_round(prod * as);
-          const float partner = __shfl_xor(v, 16);
-          if (live && (fr & 16) == 0) {
-            const float sg = v;
-            const float silu = bf16_round(sg * sigmoid(sg));
-            const float out = bf16_round(silu * partner);
-            const int o = ((n0 + wn * WTN + j * 32) >> 1) + (fr & 15);
-            static_cast<uint16_t *>(g.c)[(int64_t)m * (g.n >> 1) + o] = f16_bits(out);
-          }
-        }
-      }
-    }
-  }
+  store_tile<EPI, FM, FN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, fr, kh);
 }
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int BK, int STAGES>
 struct TileConfig {
   static constexpr int kThreads = WM * WN * 64;
-  static constexpr size_t kLds = 2 * (size_t)(BM + BN) * kBK;
+  static constexpr size_t kLds = (size_t)STAGES * (BM + BN) * BK;
 };
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int BK, int STAGES>
 hipError_t launch_tile(int epi, hipStream_t stream, const GemmArgs &a) {
-  using T = TileConfig<BM, BN, WM, WN>;
+  using T = TileConfig<BM, BN, WM, WN, BK, STAGES>;
   const int tiles = ((a.m + BM - 1) / BM) * (a.n / BN);
   dim3 grid(tiles), block(T::kThreads);
   switch (epi) {
     case kEpiPlain:
-      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, kEpiPlain>), grid, block, T::kLds, stream, a);
+      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiPlain>), grid, block, T::kLds, stream, a);
       break;
     case kEpiResid:
-      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, kEpiResid>), grid, block, T::kLds, stream, a);
+      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiResid>), grid, block, T::kLds, stream, a);
       break;
     case kEpiSwiglu:
-      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, kEpiSwiglu>), grid, block, T::kLds, stream, a);
+      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiSwiglu>), grid, block, T::kLds, stream, a);
       break;
     case kEpiBias:
-      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, kEpiBias>), grid, block, T::kLds, stream, a);
+      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiBias>), grid, block, T::kLds, stream, a);
       break;
     default:
-      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, kEpiAcc>), grid, block, T::kLds, stream, a);
+      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiAcc>), grid, block, T::kLds, stream, a);
       break;
   }
   return hipGetLastError();
 }
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int BK, int STAGES>
 hipError_t set_lds_tile() {
-  using T = TileConfig<BM, BN, WM, WN>;
-  const void *fns[5] = {reinterpret_cast<const void *>(gemm_kernel<BM, BN, WM, WN, kEpiPlain>),
-                        reinterpret_cast<const void *>(gemm_kernel<BM, BN, WM, WN, kEpiResid>),
-                        reinterpret_cast<const void *>(gemm_kernel<BM, BN, WM, WN, kEpiSwiglu>),
-                        reinterpret_cast<const void *>(gemm_kernel<BM, BN, WM, WN, kEpiBias>),
-                        reinterpret_cast<const void *>(gemm_kernel<BM, BN, WM, WN, kEpiAcc>)};
+  using T = TileConfig<BM, BN, WM, WN, BK, STAGES>;
+  const void *fns[5] = {reinterpret_cast<const void *>(gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiPlain>),
+                        reinterpret_cast<const void *>(gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiResid>),
+                        reinterpret_cast<const void *>(gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiSwiglu>),
+                        reinterpret_cast<const void *>(gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiBias>),
+                        reinterpret_cast<const void *>(gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiAcc>)};
   for (const void *f : fns) {
     hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)T::kLds);
     if (e != hipSuccess) return e;
@@ -243,15 +360,7 @@ hipError_t set_lds_tile() {
   return hipSuccess;
 }
 
-}  // namespace
-
-hipError_t configure_gemm_lds() {
-  hipError_t e = set_lds_tile<256, 256, 2, 4>();
-  if (e != hipSuccess) return e;
-  return set_lds_tile<256, 128, 4, 2>();
-}
-
-hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &l) {
+inline GemmArgs args_of(const GemmLaunch &l) {
   GemmArgs a;
   a.a = l.a;
   a.w = l.w;
@@ -265,9 +374,25 @@ hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &l) {
   a.k = (int)l.k;
   a.lda = (int)l.lda;
   a.m_group = l.m_group;
-  const int64_t big_tiles = ((l.m + 255) / 256) * (l.n / 256);
-  if (l.n % 256 == 0 && big_tiles >= 256) return launch_tile<256, 256, 2, 4>(epilogue, stream, a);
-  return launch_tile<256, 128, 4, 2>(epilogue, stream, a);
+  return a;
 }
+
+}  // namespace gemm
+
+#ifndef K2W8_GEMM_NO_ENTRY
+hipError_t configure_gemm_lds() {
+  hipError_t e = gemm::set_lds_tile<256, 256, 4, 2, 128, 2>();
+  if (e != hipSuccess) return e;
+  return gemm::set_lds_tile<256, 128, 4, 2, 128, 2>();
+}
+
+hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &l) {
+  const gemm::GemmArgs a = gemm::args_of(l);
+  const int64_t big_tiles = ((l.m + 255) / 256) * (l.n / 256);
+  if (l.n % 256 == 0 && big_tiles >= 256)
+    return gemm::launch_tile<256, 256, 4, 2, 128, 2>(epilogue, stream, a);
+  return gemm::launch_tile<256, 128, 4, 2, 128, 2>(epilogue, stream, a);
+}
+#endif
 
 }  // namespace k2w8
