@@ -30,6 +30,8 @@ sys.path.insert(0, os.path.join(ROOT, "krea2-hrx_amd"))
 
 PEAK_INT8_TOPS = 5000.0  # MI355X dense INT8 MFMA, 5.0 POP/s
 PEAK_HBM_GBS = 8000.0
+COPY_PROBE_BYTES = 256 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_i8_qkv_4096x3072x9216_traffic.json")
 METRIC = "W8A8 GEMM TOPS and % of INT8 MFMA peak at M=4096,K=3072; DiT block linear ms"
 
 
@@ -41,6 +43,9 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="headline step only")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--traffic-probe", action="store_true",
+                   help="run a 256 MiB device copy and 5 QKV steps only (for rocprofv3 --pmc "
+                        "FETCH_SIZE / WRITE_SIZE passes)")
     return p.parse_args()
 
 
@@ -110,6 +115,17 @@ def main():
         if ev is not None:
             ev[2].record(stream)
 
+    if args.traffic_probe:
+        # The copy kernel of known size that calibrates the byte counters.
+        src = torch.empty(COPY_PROBE_BYTES, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        for i in range(5):
+            step(i)
+        torch.cuda.synchronize()
+        print("traffic probe done", flush=True)
+        return
+
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
@@ -165,7 +181,7 @@ def main():
             "peak": PEAK_INT8_TOPS,
             "unit": "TFLOP/s",
             "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "algorithmic_bytes": gemm_bytes,
         },
     }
@@ -182,6 +198,16 @@ def main():
         result["cpu_baseline"] = cpu_baseline(M, K, N, pitch, args.cpu_seconds)
 
     print(json.dumps(result), flush=True)
+
+
+def measured_traffic():
+    """HBM bytes per gemm_i8 launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    passes (calibrated against a copy kernel), or None if they are absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f)["gemm_i8"]["traffic_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def timed(torch, fn, steps, warmup):

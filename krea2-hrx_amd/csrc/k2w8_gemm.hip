@@ -77,40 +77,16 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int m
   tn = in_group / rows_in_group;
 }
 
-// One BK-byte K step from an LDS stage: BK/32 slices of 32 bytes, the next slice's
-// fragments read while the current slice's MFMAs issue.
-template <int BK, int FM, int FN>
-__device__ __forceinline__ void mma_stage(v16i (&acc)[FM][FN], const uint8_t *stage,
-                                          const int (&a_row_off)[FM], const int (&b_row_off)[FN],
-                                          int kh, int rsw) {
-  v4i af[2][FM], bf[2][FN];
-  {
-    const int c = (kh ^ rsw) << 4;
+// This wave's A and B fragments of one 32-byte K slice: LDS chunk offset `c` of each
+// fragment row.
+template <int FM, int FN>
+__device__ __forceinline__ void read_frags(v4i (&af)[FM], v4i (&bf)[FN], const uint8_t *stage,
+                                           const int (&a_row_off)[FM], const int (&b_row_off)[FN],
+                                           int c) {
 #pragma unroll
-    for (int i = 0; i < FM; ++i) af[0][i] = *reinterpret_cast<const v4i *>(stage + a_row_off[i] + c);
+  for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const v4i *>(stage + a_row_off[i] + c);
 #pragma unroll
-    for (int j = 0; j < FN; ++j) bf[0][j] = *reinterpret_cast<const v4i *>(stage + b_row_off[j] + c);
-  }
-#pragma unroll
-  for (int s = 0; s < BK / 32; ++s) {
-    const int cur = s & 1;
-    if (s + 1 < BK / 32) {
-      const int c = (((s + 1) * 2 + kh) ^ rsw) << 4;
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-        af[cur ^ 1][i] = *reinterpret_cast<const v4i *>(stage + a_row_off[i] + c);
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-        bf[cur ^ 1][j] = *reinterpret_cast<const v4i *>(stage + b_row_off[j] + c);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[cur][j], af[cur][i], acc[i][j], 0, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-  }
+  for (int j = 0; j < FN; ++j) bf[j] = *reinterpret_cast<const v4i *>(stage + b_row_off[j] + c);
 }
 
 // Epilogue of one wave's (32 FM) x (32 FN) sub-tile at rows m_base.., columns n_base..
@@ -276,7 +252,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
     for (int i = 0; i < kBIns; ++i) dma16(b_lds + so + i * 1024, g.w, b_off[i] + ko);
   };
 #pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s)
+  for (int s = 0; s < STAGES; ++s)
     if (s < kt_count) issue(s);
 
   v16i acc[FM][FN];
@@ -286,6 +262,11 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
     for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
+#ifdef K2W8_AGPR_ACC
+  // An AGPR operand anywhere in the function makes the compiler select the MFMA form
+  // whose accumulator lives in AGPRs, keeping the accumulators out of the VGPR file.
+  asm volatile("; agpr hint %0" ::"a"(0));
+#endif
 
   const int wm = wave / WN, wn = wave % WN;
   const int fr = lane & 31, kh = lane >> 5;
@@ -298,17 +279,49 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
   for (int j = 0; j < FN; ++j) b_row_off[j] = BM * BK + (wn * WTN + j * 32 + fr) * BK;
   const int rsw = swz_key<BK>(fr);
 
+  // Software pipeline. Fragments of the next 32-byte K slice are read while the
+  // current slice's MFMAs issue; the next slice of the last slice of a step is the
+  // first slice of the next stage. Before reading it, during that last slice, each
+  // wave waits for its own transfers of the next stage, drains its LDS reads of the
+  // current stage, and meets the others at the barrier: then every wave's transfers
+  // for the next stage have landed and nobody reads the current stage any more, so
+  // the transfer for stage kt+STAGES can refill it. Barrier and first reads hide
+  // behind the last slice's MFMAs.
+  constexpr int NS = BK / 32;
+  static_assert(NS % 2 == 0, "slice parity must repeat per step");
+  v4i af[2][FM], bf[2][FN];
+  if (STAGES >= 2) wait_vmcnt<(STAGES - 1) * kIns>();
+  if (kt_count < STAGES) wait_vmcnt<0>();
+  __builtin_amdgcn_s_barrier();
+  read_frags<FM, FN>(af[0], bf[0], smem, a_row_off, b_row_off, (kh ^ rsw) << 4);
+
   for (int kt = 0; kt < kt_count; ++kt) {
-    // This wave's transfers for step kt are done once at most the later stages'
-    // transfers are outstanding; the barrier then covers every wave's, and every
-    // wave's reads of the stage the next transfer overwrites.
-    if (kt + STAGES - 2 < kt_count)
-      wait_vmcnt<(STAGES - 2) * kIns>();
-    else
-      wait_vmcnt<0>();
-    __builtin_amdgcn_s_barrier();
-    if (kt + STAGES - 1 < kt_count) issue(kt + STAGES - 1);
-    mma_stage<BK, FM, FN>(acc, smem + (kt % STAGES) * kStage, a_row_off, b_row_off, kh, rsw);
+    const uint8_t *stage = smem + (kt % STAGES) * kStage;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int cur = s & 1;
+      if (s + 1 < NS) {
+        read_frags<FM, FN>(af[cur ^ 1], bf[cur ^ 1], stage, a_row_off, b_row_off,
+                           ((2 * (s + 1) + kh) ^ rsw) << 4);
+      } else if (kt + 1 < kt_count) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (kt + STAGES - 1 < kt_count)
+          wait_vmcnt<(STAGES - 2) * kIns>();
+        else
+          wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        if (kt + STAGES < kt_count) issue(kt + STAGES);
+        read_frags<FM, FN>(af[cur ^ 1], bf[cur ^ 1], smem + ((kt + 1) % STAGES) * kStage,
+                           a_row_off, b_row_off, (kh ^ rsw) << 4);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[cur][j], af[cur][i], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 
   store_tile<EPI, FM, FN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, fr, kh);
