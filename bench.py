@@ -191,7 +191,13 @@ def main():
     if not args.no_extra:
         result["north_star"] = north_star(k2, torch, weights, hidden, args)
         torch.cuda.empty_cache()
+        result["config1_single_gemm"] = single_gemm(k2, torch, weights, hidden, args)
+        torch.cuda.empty_cache()
+        result["config3_mlp_pair"] = mlp_pair(k2, torch, weights, hidden, args)
+        torch.cuda.empty_cache()
         result["block_linears"] = block_linears(k2, torch, weights, hidden, args)
+        torch.cuda.empty_cache()
+        result["config5_skinny"] = skinny_sweep(k2, torch, weights, hidden, args)
         torch.cuda.empty_cache()
 
     if not args.no_cpu:
@@ -208,6 +214,26 @@ def measured_traffic():
             return json.load(f)["gemm_i8"]["traffic_bytes"]
     except (OSError, KeyError, ValueError):
         return None
+
+
+def event_timed(torch, fn, steps, warmup):
+    """Mean GPU time of fn's launches: HIP events recorded on the launch stream around each
+    call, so host-side launch overhead between calls is excluded."""
+    for i in range(warmup):
+        fn(i)
+    stream = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    # Keep the GPU busy while the host enqueues, so that each event pair brackets only
+    # its kernels and not the host's launch latency (~40 us of spin per step queued).
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(steps * 40e-6 * 2.4e9))
+    for i, (e0, e1) in enumerate(evs):
+        e0.record(stream)
+        fn(i)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    return sum(e0.elapsed_time(e1) for e0, e1 in evs) * 1e-3 / steps
 
 
 def timed(torch, fn, steps, warmup):
@@ -239,6 +265,100 @@ def north_star(k2, torch, weights, hidden, args):
     tops = 2.0 * M * N * K / sec / 1e12
     return {"M": M, "K": K, "N": N, "us": round(sec * 1e6, 2), "TOPS": round(tops, 1),
             "pct_of_int8_peak": round(100 * tops / PEAK_INT8_TOPS, 2), "target_pct": 60.0}
+
+
+def single_gemm(k2, torch, weights, hidden, args):
+    """f16 A [4096, 3072] quantised per token (prepare_plain_i8) -> gemm_i8 with
+    int8 W [3072, 3072], per-channel scales and an f16 bias (gemm_i8_bias) -> f16 out."""
+    M, K, N = 4096, 3072, 3072
+    h = hidden(M, K, 1000).to(torch.float16)
+    q = torch.empty((M, K), dtype=torch.int8, device="cuda")
+    qs = torch.empty(M, dtype=torch.float32, device="cuda")
+    w, ws = weights(N, K, 1001)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1002)
+    bias = (torch.randn(N, generator=g, device="cuda") * 0.02).to(torch.float16)
+    out = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    cfg = k2.GemmConfig(K, N, K)
+
+    def fn(_):
+        k2.prepare_plain_i8(h, q, qs, width=K, out_stride=K)
+        k2.gemm_i8_bias(q, w, ws, qs, bias, out, cfg=cfg)
+
+    sec = timed(torch, fn, args.steps, args.warmup)
+    gsec = timed(torch, lambda _: k2.gemm_i8_bias(q, w, ws, qs, bias, out, cfg=cfg), args.steps,
+                 args.warmup)
+    ops = 2.0 * M * N * K
+    return {"M": M, "K": K, "N": N, "us_prepare_plus_gemm": round(sec * 1e6, 2),
+            "us_gemm": round(gsec * 1e6, 2), "TOPS_gemm": round(ops / gsec / 1e12, 1),
+            "TOPS_with_prepare": round(ops / sec / 1e12, 1)}
+
+
+def mlp_pair(k2, torch, weights, hidden, args):
+    """configs[2]: M=4608 -> gemm_i8_swiglu (W [2x12288, 3072], interleaved) -> f16 [4608, 12288]
+    -> prepare_plain_i8 -> gemm_i8_resid_256x256 (W [3072, 12288]) on a bf16 residual."""
+    M, H, I = 4608, 3072, 12288
+    pitch_i = k2.shape.gemm_pitch(I)
+    qa = torch.randint(-127, 128, (M, H), device="cuda", dtype=torch.int8)
+    qas = torch.rand(M, device="cuda") * 1e-2 + 1e-3
+    wgu, sgu = weights(2 * I, H, 3100)
+    wd, sd = weights(H, pitch_i, 3101)
+    up = torch.empty((M, I), dtype=torch.float16, device="cuda")
+    q = torch.empty((M, pitch_i), dtype=torch.int8, device="cuda")
+    qs = torch.empty(M, dtype=torch.float32, device="cuda")
+    x = hidden(M, H, 3102).to(torch.bfloat16)
+    one = torch.ones(H, device="cuda")
+    c_gu = k2.GemmConfig(H, 2 * I, H)
+    c_d = k2.GemmConfig(I, H, pitch_i, schedule_rows=int(k2.shape.gemm_schedule_rows(M)))
+
+    def fn(_):
+        k2.gemm_i8_swiglu(qa, wgu, sgu, qas, up, cfg=c_gu)
+        k2.prepare_plain_i8(up, q, qs, width=I, out_stride=pitch_i)
+        k2.gemm_i8_resid_256x256(q, wd, sd, qs, x, one, cfg=c_d)
+
+    sec = timed(torch, fn, max(2, args.steps // 2), max(1, args.warmup // 2))
+    ops = 2.0 * M * H * 2 * I + 2.0 * M * I * H
+    return {"M": M, "ms": round(sec * 1e3, 4), "TOPS": round(ops / sec / 1e12, 1),
+            "pct_of_int8_peak": round(100 * ops / sec / 1e12 / PEAK_INT8_TOPS, 2)}
+
+
+def skinny_sweep(k2, torch, weights, hidden, args):
+    """text-encoder-shaped few-token regime, hidden 2560, intermediate 9728:
+    QKV [4096 x 2560], SwiGLU up [2 x 9728 x 2560], down [2560 x 9728] (with residual) for
+    M in {1, 16, 77, 256, 512}. HBM-bound on the weights at small M: reported as GB/s of
+    algorithmic bytes against the 8 TB/s peak."""
+    H, I = 2560, 9728
+    pitch_i = k2.shape.gemm_pitch(I)
+    wq, sq = weights(4096, H, 5100)
+    wgu, sgu = weights(2 * I, H, 5101)
+    wd, sd = weights(H, pitch_i, 5102)
+    one = torch.ones(H, device="cuda")
+    rows = []
+    for M in (1, 16, 77, 256, 512):
+        a_h = torch.randint(-127, 128, (M, H), device="cuda", dtype=torch.int8)
+        a_i = torch.randint(-127, 128, (M, pitch_i), device="cuda", dtype=torch.int8)
+        sc = torch.rand(M, device="cuda") * 1e-2 + 1e-3
+        o_q = torch.empty((M, 4096), dtype=torch.float16, device="cuda")
+        o_u = torch.empty((M, I), dtype=torch.float16, device="cuda")
+        x = torch.zeros((M, H), dtype=torch.bfloat16, device="cuda")
+        cases = [
+            ("qkv", lambda _: k2.gemm_i8(a_h, wq, sq, sc, o_q, cfg=k2.GemmConfig(H, 4096, H)),
+             4096, H, 2 * M * 4096),
+            ("up_swiglu", lambda _: k2.gemm_i8_swiglu(a_h, wgu, sgu, sc, o_u,
+                                                      cfg=k2.GemmConfig(H, 2 * I, H)),
+             2 * I, H, 2 * M * I),
+            ("down_resid", lambda _: k2.gemm_i8_resid(a_i, wd, sd, sc, x, one,
+                                                      cfg=k2.GemmConfig(I, H, pitch_i)),
+             H, I, 4 * M * H),
+        ]
+        for name, fn, n, k, out_bytes in cases:
+            sec = event_timed(torch, fn, max(20, args.steps), max(5, args.warmup))
+            byts = n * k + M * k + 4 * n + 4 * M + out_bytes
+            rows.append({"M": M, "gemm": name, "N": n, "K": k, "us": round(sec * 1e6, 2),
+                         "GBps": round(byts / sec / 1e9, 1),
+                         "pct_of_hbm_peak": round(100 * byts / sec / 1e9 / PEAK_HBM_GBS, 1),
+                         "TOPS": round(2.0 * M * n * k / sec / 1e12, 1)})
+    return rows
 
 
 def block_linears(k2, torch, weights, hidden, args):

@@ -393,18 +393,29 @@ inline GemmArgs args_of(const GemmLaunch &l) {
 }  // namespace gemm
 
 #ifndef K2W8_GEMM_NO_ENTRY
+// Token counts served by the few-token kernel (weights streamed, HBM-bound).
+constexpr int64_t kSkinnyMaxTokens = 128;
+
 hipError_t configure_gemm_lds() {
   hipError_t e = gemm::set_lds_tile<256, 256, 4, 2, 128, 2>();
-  if (e != hipSuccess) return e;
-  return gemm::set_lds_tile<256, 128, 4, 2, 128, 2>();
+  if (e == hipSuccess) e = gemm::set_lds_tile<256, 128, 4, 2, 128, 2>();
+  if (e == hipSuccess) e = gemm::set_lds_tile<128, 128, 2, 2, 128, 2>();
+  if (e == hipSuccess) e = gemm::set_lds_tile<64, 64, 2, 2, 128, 2>();
+  return e;
 }
 
+// Tile choice: the largest tile that still gives every CU a workgroup; below that,
+// the smallest tile (more workgroups than CUs matters more than per-tile efficiency).
 hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &l) {
+  if (l.m <= kSkinnyMaxTokens) return launch_skinny(epilogue, stream, l);
   const gemm::GemmArgs a = gemm::args_of(l);
-  const int64_t big_tiles = ((l.m + 255) / 256) * (l.n / 256);
-  if (l.n % 256 == 0 && big_tiles >= 256)
+  auto tiles = [&](int64_t bm, int64_t bn) { return ((l.m + bm - 1) / bm) * (l.n / bn); };
+  constexpr int64_t kCus = 256;
+  if (l.n % 256 == 0 && tiles(256, 256) >= kCus)
     return gemm::launch_tile<256, 256, 4, 2, 128, 2>(epilogue, stream, a);
-  return gemm::launch_tile<256, 128, 4, 2, 128, 2>(epilogue, stream, a);
+  if (tiles(256, 128) >= kCus) return gemm::launch_tile<256, 128, 4, 2, 128, 2>(epilogue, stream, a);
+  if (tiles(128, 128) >= kCus) return gemm::launch_tile<128, 128, 2, 2, 128, 2>(epilogue, stream, a);
+  return gemm::launch_tile<64, 64, 2, 2, 128, 2>(epilogue, stream, a);
 }
 #endif
 

@@ -33,6 +33,8 @@ struct GemmLaunch {
 };
 
 hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &g);
+// Few-token kernel (any m; chosen by launch_gemm for small m).
+hipError_t launch_skinny(int epilogue, hipStream_t stream, const GemmLaunch &g);
 hipError_t configure_gemm_lds();
 
 }  // namespace k2w8

@@ -91,6 +91,12 @@ SHAPES = [
     (1000, 3072, 768, 0),
     (513, 2560, 4096, 0),
     (2000, 256, 8192, 64),  # >= 256 tiles of 256x256: the wide-tile kernel
+    # few-token kernel: K ranges that leave single 64-byte steps per wave, 1..4 blocks
+    (2, 384, 256, 0),
+    (16, 2560, 512, 0),
+    (33, 640, 384, 64),
+    (64, 9728, 256, 0),
+    (77, 2560, 512, 0),
 ]
 
 
