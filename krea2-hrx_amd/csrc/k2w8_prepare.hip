@@ -1,18 +1,36 @@
-// Activation prepares of the W8A8 path for gfx950: form a token's row (modulated
-// RMSNorm, plain f16, or attention x sigmoid(gate)), rotate it by the group-256
-// regular Hadamard H4 (x) H4 (x) H4 (x) H4, and quantise it per token to int8
-// with an f32 scale.
+// Activation prepares of the W8A8 path for gfx950. Each prepare forms a token's row
+// in one of three ways: modulated RMSNorm, plain f16, or attention x sigmoid(gate).
+// It then rotates the row by the group-256 regular Hadamard H4 (x) H4 (x) H4 (x) H4
+// and quantises it per token to int8, with an f32 scale.
 //
-// One 256-lane workgroup (four wave64s) per token. The rotation runs on sets of
-// sixteen values held in registers, two radix-4 stages per set:
-//   pass 1: a lane owns 16 adjacent elements (a "run"): stages of stride 1 and 4;
-//   pass 2: a lane owns the 16 elements b, b+16, ..., b+240 of a 256-group: the
-//           stages of stride 16 and 64 are again register strides 1 and 4.
-// The row crosses LDS (f32) once between the passes and once more before the
-// quantiser, which works on runs again so each lane stores 16 contiguous bytes.
+// Layout. A token row belongs to a team of WPT wave64s (one wave for widths up to 4096).
+// Each lane holds T runs of 16 adjacent elements, in registers, from load to store.
+// The 16 runs of a 256-group lie in one 16-lane DPP row. Lane i of the row holds run
+// swap23(i), where swap23 exchanges bits 2 and 3. This maps the row's lane bits 0, 1,
+// 3, 2 onto the element bits 4, 5, 6, 7 of the group. The loads and stores of a row
+// still cover the group's bytes contiguously.
 //
-// Reference arithmetic: kernels/prepare_{norm,plain,gated}_i8.loom (each step
-// below cites its lines).
+// Hadamard stages by stride:
+//   1 and 4   in registers.
+//   16        lanes xor 1 then xor 2, through quad_perm DPP.
+//   64        lanes xor 8 (row_ror:8), then lanes xor 4 (ds_swizzle).
+// The cross-lane steps keep the reference's operation order. With S = own + partner
+// and D = partner - own from the first exchange, o = S - D(xor partner) equals
+// (e0+e1)+(e2-e3), (e0+e1)-(e2-e3), (e0-e1)+(e2+e3) and (e2+e3)-(e0-e1) bit for bit
+// (IEEE addition is commutative, and x - (-y) == x + y).
+//
+// The norm's sum of squares needs the reference's reduction order. For a single-wave
+// team it is kept from the registers: lane l holds the reference's 32-lane-wave
+// partials for virtual lanes 2r and 2r+1 of its runs r. For larger teams it runs as
+// a separate canonical pass. The row amax is a wave max (plus LDS for multi-wave
+// teams).
+//
+// Teams loop over tokens, and the next token's row is in flight while the current one
+// computes. A block of single-wave teams stages the norm vectors (per element, not per
+// token) in LDS once, as the factors the element formula multiplies by.
+//
+// Reference arithmetic: kernels/prepare_{norm,plain,gated}_i8.loom (each step below
+// cites its lines).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -23,56 +41,85 @@ namespace k2w8 {
 
 namespace {
 
-constexpr int kThreads = 256;
-
 enum PrepareKind { kNorm = 0, kPlain = 1, kGated = 2 };
 
-// LDS index of row element e: four floats of padding after every 64 so that
-// the sixteen lanes of one 256-group (pass 2) and the next group start 16 banks apart.
-__device__ __forceinline__ int lds_index(int e) { return e + ((e >> 6) << 2); }
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
 
-// One radix-4 stage of H4 on quads (v[i], v[i+s], v[i+2s], v[i+3s]) of a 16-set,
-// with the reference's operation order (kernels/prepare_norm_i8.loom:194-201):
-//   o0 = (e0+e1)+(e2-e3), o1 = (e0+e1)-(e2-e3), o2 = (e0-e1)+(e2+e3), o3 = (e2+e3)-(e0-e1).
-// The plain prepare scales each output by 1/4 and rounds it to f16
+// DPP controls: quad_perm [1,0,3,2], [2,3,0,1]; row_ror by 8.
+constexpr int kQuadXor1 = 0xB1, kQuadXor2 = 0x4E, kRowRor8 = 0x128;
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kCtrl, 0xf, 0xf, true));
+}
+
+// Two values rounded to bf16 (round to nearest even, the hardware conversion) and
+// widened back to f32. Identical to the bit-pattern rounding of src/numerics.rs:18-26
+// for every non-NaN input.
+__device__ __forceinline__ void bf16_round2(float &a, float &b) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, bf2));
+  a = __uint_as_float(u << 16);
+  b = __uint_as_float(u & 0xffff0000u);
+}
+
+__device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_bf16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Optional stage rounding of the plain prepare: f16(0.25 * o)
 // (kernels/prepare_plain_i8.loom:120-127).
-template <int S, bool kF16Quarter>
-__device__ __forceinline__ void radix4(float (&v)[16]) {
+template <bool kQuarter>
+__device__ __forceinline__ float stage_out(float o) {
+  return kQuarter ? f16_round(o * 0.25f) : o;
+}
+
+// In-register radix-4 stage over quads (v[i], v[i+s], v[i+2s], v[i+3s]) of a run, in
+// the reference's order (kernels/prepare_norm_i8.loom:194-201):
+//   o0 = (e0+e1)+(e2-e3), o1 = (e0+e1)-(e2-e3), o2 = (e0-e1)+(e2+e3), o3 = (e2+e3)-(e0-e1).
+template <int S, bool kQuarter>
+__device__ __forceinline__ void radix4_reg(float (&v)[16]) {
 #pragma unroll
   for (int block = 0; block < 16; block += 4 * S) {
 #pragma unroll
     for (int c = 0; c < S; ++c) {
       const int i = block + c;
-      float e0 = v[i], e1 = v[i + S], e2 = v[i + 2 * S], e3 = v[i + 3 * S];
-      float s01 = e0 + e1, s23 = e2 + e3, d01 = e0 - e1, d23 = e2 - e3;
-      float o0 = s01 + d23, o1 = s01 - d23, o2 = d01 + s23, o3 = s23 - d01;
-      if (kF16Quarter) {
-        o0 = f16_round(o0 * 0.25f);
-        o1 = f16_round(o1 * 0.25f);
-        o2 = f16_round(o2 * 0.25f);
-        o3 = f16_round(o3 * 0.25f);
-      }
-      v[i] = o0;
-      v[i + S] = o1;
-      v[i + 2 * S] = o2;
-      v[i + 3 * S] = o3;
+      const float e0 = v[i], e1 = v[i + S], e2 = v[i + 2 * S], e3 = v[i + 3 * S];
+      const float s01 = e0 + e1, s23 = e2 + e3, d01 = e0 - e1, d23 = e2 - e3;
+      v[i] = stage_out<kQuarter>(s01 + d23);
+      v[i + S] = stage_out<kQuarter>(s01 - d23);
+      v[i + 2 * S] = stage_out<kQuarter>(d01 + s23);
+      v[i + 3 * S] = stage_out<kQuarter>(s23 - d01);
     }
   }
 }
 
-__device__ __forceinline__ void unpack_halves(const uint4 &p, uint16_t (&out)[8]) {
-  const uint32_t w[4] = {p.x, p.y, p.z, p.w};
+// Stride-16 stage: e0..e3 sit in lanes q = 0..3 of a quad (element bits 4, 5 = lane
+// bits 0, 1). S = own + partner(xor 1) is s01 or s23; D = partner - own is -d01, d01,
+// -d23, d23 for q = 0..3; o_q = S - D(q xor 2).
+template <bool kQuarter>
+__device__ __forceinline__ void radix4_quad(float (&v)[16]) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    out[2 * i] = (uint16_t)(w[i] & 0xffffu);
-    out[2 * i + 1] = (uint16_t)(w[i] >> 16);
+  for (int i = 0; i < 16; ++i) {
+    const float s = dpp<kQuadXor1>(v[i]) + v[i];
+    const float d = dpp<kQuadXor1>(v[i]) - v[i];
+    v[i] = stage_out<kQuarter>(s - dpp<kQuadXor2>(d));
   }
 }
 
-__device__ __forceinline__ float wave_max(float v) {
+// Stride-64 stage: element bit 6 = lane bit 3, bit 7 = lane bit 2. The first exchange
+// is lanes xor 8 (row_ror:8, a DPP operand); the second, lanes xor 4, goes through
+// ds_swizzle (bitmask mode: and 0x1f, xor 4), which has no DPP form on this chip.
+template <bool kQuarter>
+__device__ __forceinline__ void radix4_row(float (&v)[16]) {
 #pragma unroll
-  for (int s = 32; s >= 1; s >>= 1) v = fmaxf(v, __shfl_xor(v, s));
-  return v;
+  for (int i = 0; i < 16; ++i) {
+    const float s = dpp<kRowRor8>(v[i]) + v[i];
+    const float d = dpp<kRowRor8>(v[i]) - v[i];
+    const float dx = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, d), 0x101F));
+    v[i] = stage_out<kQuarter>(s - dx);
+  }
 }
 
 struct PrepareArgs {
@@ -81,168 +128,411 @@ struct PrepareArgs {
   const float *norm_scale, *mod_scale, *mod_shift;  // norm only
   int8_t *q;
   float *q_scale;
-  int width, out_stride, gate_stride;
+  int tokens, width, out_stride, gate_stride;
   float eps;
+  int wpt;    // waves per token team
+  int teams;  // teams per block
 };
 
-template <int kKind>
-__global__ __launch_bounds__(kThreads) void prepare_kernel(PrepareArgs args) {
-  extern __shared__ float row_lds[];
-  __shared__ float partial[8];
-  const int lane = threadIdx.x;
-  const int64_t token = blockIdx.x;
+// Raw input of one lane for one token: T runs of 16 f16/bf16 (and the gate's).
+template <int kKind, int T>
+struct Raw {
+  v4u x[T][2];
+  v4u g[kKind == kGated ? T : 1][2];
+};
+
+constexpr int kMaxThreads = 1024;
+constexpr int kMaxTeams = 4;
+constexpr int kMaxWpt = 16;
+
+// Threads per block a kernel is compiled for: teams of up to 16 waves hold one or two
+// runs per lane; three or four runs per lane need the register room of at most 8 waves.
+template <int T>
+struct Bounds {
+  static constexpr int kThreads = T <= 2 ? kMaxThreads : 512;
+};
+
+// kSingle: one-wave teams (no block barriers, the norm's sum of squares from
+// registers, norm factors staged in LDS). Otherwise teams of wpt waves.
+template <int kKind, int T, bool kSingle>
+__global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArgs args) {
+  constexpr bool kQuarter = (kKind == kPlain);
+  __shared__ float lds_part[2][kMaxTeams][8];         // norm partials (multi-wave teams)
+  __shared__ float lds_amax[2][kMaxTeams][kMaxWpt];   // wave maxima (multi-wave teams)
+
+  const int wpt = args.wpt, teams = args.teams;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int team = wave / wpt, wave_in_team = wave % wpt;
   const int width = args.width;
   const int runs = width >> 4;
-
-  float rms_inv = 0.0f;
-  if (kKind == kNorm) {
-    // Sum of squares in the reference's lane layout (kernels/prepare_norm_i8.loom:90-101):
-    // lane L accumulates eight partials over chunks L, L+256, ... of 8 values.
-    const uint16_t *hr = args.h + token * width;
-    const int chunks = width >> 3;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int c = lane; c < chunks; c += kThreads) {
-      uint16_t x[8];
-      unpack_halves(*reinterpret_cast<const uint4 *>(hr + c * 8), x);
+  // Run held by this lane at t: wave base + 64 t + 16 (lane row) + swap23(lane in row).
+  const int li = lane & 15;
+  const int run0 = 64 * T * wave_in_team + 16 * (lane >> 4) +
+                   ((li & 3) | ((li >> 3) & 1) << 2 | ((li >> 2) & 1) << 3);
+  bool valid[T];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float xf = bf16_value(x[e]);
-        float sq = xf * xf;
-        acc[e] = acc[e] + sq;
+  for (int t = 0; t < T; ++t) valid[t] = run0 + 64 * t < runs;
+
+  // Loads are unconditional (out-of-range rows and runs read row 0 / run 0 and are
+  // not used), so no branch separates a prefetch from the waits on earlier loads:
+  // the compiler's wait counting stays exact and the prefetch overlaps the compute.
+  auto load = [&](Raw<kKind, T> &r, int token) {
+    token = token < args.tokens ? token : 0;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int e0 = valid[t] ? (run0 + 64 * t) << 4 : 0;
+      const v4u *p = reinterpret_cast<const v4u *>(args.h + (int64_t)token * width + e0);
+      r.x[t][0] = p[0];
+      r.x[t][1] = p[1];
+      if (kKind == kGated) {
+        const v4u *g = reinterpret_cast<const v4u *>(args.gate + (int64_t)token * args.gate_stride + e0);
+        r.g[t][0] = g[0];
+        r.g[t][1] = g[1];
       }
     }
-    float s = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) s = s + acc[e];
-    // Each half of a wave64 is one of the reference's 32-lane waves: xor butterfly
-    // with strides 1..16 stays inside the half.
-#pragma unroll
-    for (int stride = 1; stride < 32; stride <<= 1) s = s + __shfl_xor(s, stride);
-    if ((lane & 31) == 0) partial[lane >> 5] = s;
+  };
+
+  const int stride = gridDim.x * teams;
+  int iter = 0;
+  Raw<kKind, T> cur;
+  int token = blockIdx.x * teams + team;
+  load(cur, token);
+
+  // Norm vectors (kernels/prepare_norm_i8.loom:150-158) as the per-element factors
+  // ns + 1, bf16(ms + 1) and the shift. They do not depend on the token: a block of
+  // one-wave teams stages them in LDS once (run r at float4 slots 12 r .. 12 r + 11),
+  // wider teams read them from global memory per token.
+  extern __shared__ float4 factor_lds[];
+  constexpr bool kLdsFactors = (kKind == kNorm) && kSingle;
+  if (kLdsFactors) {
+    for (int c = threadIdx.x; c < (width >> 2); c += blockDim.x) {
+      const float4 a = reinterpret_cast<const float4 *>(args.norm_scale)[c];
+      const float4 b = reinterpret_cast<const float4 *>(args.mod_scale)[c];
+      float m0 = b.x + 1.0f, m1 = b.y + 1.0f, m2 = b.z + 1.0f, m3 = b.w + 1.0f;
+      bf16_round2(m0, m1);
+      bf16_round2(m2, m3);
+      const int slot = 12 * (c >> 2) + (c & 3);
+      factor_lds[slot] = make_float4(a.x + 1.0f, a.y + 1.0f, a.z + 1.0f, a.w + 1.0f);
+      factor_lds[slot + 4] = make_float4(m0, m1, m2, m3);
+      factor_lds[slot + 8] = reinterpret_cast<const float4 *>(args.mod_shift)[c];
+    }
     __syncthreads();
-    // :132-143, in the reference's explicit order.
-    float pair0 = partial[0] + partial[4], pair1 = partial[1] + partial[5];
-    float pair2 = partial[2] + partial[6], pair3 = partial[3] + partial[7];
-    float total = (pair0 + pair2) + (pair1 + pair3);
-    float mean = total / (float)width;
-    float mean_eps = mean + args.eps;
-    rms_inv = 1.0f / __builtin_sqrtf(mean_eps);
   }
-
-  // Pass 1: form runs of 16 adjacent elements, stages of stride 1 and 4.
-  for (int r = lane; r < runs; r += kThreads) {
-    const int e0 = r << 4;
-    float v[16];
-    if (kKind == kNorm) {
-      // :145-170
-      const uint16_t *hr = args.h + token * width + e0;
-      uint16_t x[16];
-      unpack_halves(*reinterpret_cast<const uint4 *>(hr), *reinterpret_cast<uint16_t(*)[8]>(x));
-      unpack_halves(*reinterpret_cast<const uint4 *>(hr + 8),
-                    *reinterpret_cast<uint16_t(*)[8]>(x + 8));
-      const float4 *ns4 = reinterpret_cast<const float4 *>(args.norm_scale + e0);
-      const float4 *ms4 = reinterpret_cast<const float4 *>(args.mod_scale + e0);
-      const float4 *sh4 = reinterpret_cast<const float4 *>(args.mod_shift + e0);
-      float ns[16], ms[16], sh[16];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float4 a = ns4[i], b = ms4[i], c = sh4[i];
-        ns[4 * i] = a.x; ns[4 * i + 1] = a.y; ns[4 * i + 2] = a.z; ns[4 * i + 3] = a.w;
-        ms[4 * i] = b.x; ms[4 * i + 1] = b.y; ms[4 * i + 2] = b.z; ms[4 * i + 3] = b.w;
-        sh[4 * i] = c.x; sh[4 * i + 1] = c.y; sh[4 * i + 2] = c.z; sh[4 * i + 3] = c.w;
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float xf = bf16_value(x[i]);
-        float n = xf * rms_inv;
-        float ns1 = ns[i] + 1.0f;
-        float normed = bf16_round(n * ns1);
-        float ms1 = bf16_round(ms[i] + 1.0f);
-        float scaled = bf16_round(normed * ms1);
-        v[i] = bf16_round(scaled + sh[i]);
-      }
-    } else if (kKind == kPlain) {
-      // kernels/prepare_plain_i8.loom:89-90
-      const uint16_t *hr = args.h + token * width + e0;
-      uint16_t x[16];
-      unpack_halves(*reinterpret_cast<const uint4 *>(hr), *reinterpret_cast<uint16_t(*)[8]>(x));
-      unpack_halves(*reinterpret_cast<const uint4 *>(hr + 8),
-                    *reinterpret_cast<uint16_t(*)[8]>(x + 8));
-#pragma unroll
-      for (int i = 0; i < 16; ++i) v[i] = f16_value(x[i]);
-    } else {
-      // kernels/prepare_gated_i8.loom:86-108
-      const uint16_t *ar = args.h + token * width + e0;
-      const uint16_t *gr = args.gate + token * (int64_t)args.gate_stride + e0;
-      uint16_t a[16], g[16];
-      unpack_halves(*reinterpret_cast<const uint4 *>(ar), *reinterpret_cast<uint16_t(*)[8]>(a));
-      unpack_halves(*reinterpret_cast<const uint4 *>(ar + 8),
-                    *reinterpret_cast<uint16_t(*)[8]>(a + 8));
-      unpack_halves(*reinterpret_cast<const uint4 *>(gr), *reinterpret_cast<uint16_t(*)[8]>(g));
-      unpack_halves(*reinterpret_cast<const uint4 *>(gr + 8),
-                    *reinterpret_cast<uint16_t(*)[8]>(g + 8));
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float af = bf16_round(f16_value(a[i]));
-        float sig = bf16_round(sigmoid(f16_value(g[i])));
-        v[i] = bf16_round(af * sig);
-      }
-    }
-    radix4<1, kKind == kPlain>(v);
-    radix4<4, kKind == kPlain>(v);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) row_lds[lds_index(e0 + i)] = v[i];
-  }
-  __syncthreads();
-
-  // Pass 2: sets {b + 16j} of each 256-group, stages of stride 16 and 64.
-  float amax = 0.0f;
-  for (int s = lane; s < runs; s += kThreads) {
-    const int base = ((s >> 4) << 8) + (s & 15);
-    float v[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = row_lds[lds_index(base + 16 * j)];
-    radix4<1, kKind == kPlain>(v);
-    radix4<4, kKind == kPlain>(v);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      amax = fmaxf(amax, fabsf(v[j]));
-      row_lds[lds_index(base + 16 * j)] = v[j];
-    }
-  }
-  amax = wave_max(amax);
-  if ((lane & 63) == 0) partial[lane >> 6] = amax;
-  __syncthreads();
-
-  // Scale (kernels/prepare_plain_i8.loom:294-299, kernels/prepare_norm_i8.loom:322-327).
-  const float rotation_scale = (kKind == kPlain) ? 16.0f : 0.0625f;
-  float row_max = fmaxf(fmaxf(partial[0], partial[1]), fmaxf(partial[2], partial[3]));
-  row_max = row_max * rotation_scale;
-  float safe = fmaxf(row_max, 1e-30f);
-  float scale = safe / 127.0f;
-  float inv = rotation_scale / scale;
-
-  // Quantise runs of 16 and store 16 bytes per lane (:301-340, bytes low first).
-  int8_t *qr = args.q + token * (int64_t)args.out_stride;
-  for (int r = lane; r < runs; r += kThreads) {
-    const int e0 = r << 4;
-    uint32_t w[4];
+  auto factors = [&](int r, float (&ns1)[16], float (&ms1)[16], float (&shf)[16]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      uint32_t word = 0;
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        float x = row_lds[lds_index(e0 + 4 * i + b)];
-        float qv = __builtin_rintf(x * inv);
-        qv = fmaxf(qv, -127.0f);
-        qv = fminf(qv, 127.0f);
-        word |= ((uint32_t)(int)qv & 0xffu) << (8 * b);
+      float4 a, b, c;
+      if (kLdsFactors) {
+        a = factor_lds[12 * r + i];
+        b = factor_lds[12 * r + 4 + i];
+        c = factor_lds[12 * r + 8 + i];
+      } else {
+        a = reinterpret_cast<const float4 *>(args.norm_scale)[4 * r + i];
+        b = reinterpret_cast<const float4 *>(args.mod_scale)[4 * r + i];
+        c = reinterpret_cast<const float4 *>(args.mod_shift)[4 * r + i];
+        a = make_float4(a.x + 1.0f, a.y + 1.0f, a.z + 1.0f, a.w + 1.0f);
+        float m0 = b.x + 1.0f, m1 = b.y + 1.0f, m2 = b.z + 1.0f, m3 = b.w + 1.0f;
+        bf16_round2(m0, m1);
+        bf16_round2(m2, m3);
+        b = make_float4(m0, m1, m2, m3);
       }
-      w[i] = word;
+      ns1[4 * i] = a.x; ns1[4 * i + 1] = a.y; ns1[4 * i + 2] = a.z; ns1[4 * i + 3] = a.w;
+      ms1[4 * i] = b.x; ms1[4 * i + 1] = b.y; ms1[4 * i + 2] = b.z; ms1[4 * i + 3] = b.w;
+      shf[4 * i] = c.x; shf[4 * i + 1] = c.y; shf[4 * i + 2] = c.z; shf[4 * i + 3] = c.w;
     }
-    *reinterpret_cast<uint4 *>(qr + e0) = make_uint4(w[0], w[1], w[2], w[3]);
+  };
+  // The wait counter for global loads is in order: a load issued after the prefetch
+  // of the next row would make every wait on it wait for the prefetch too. The
+  // multi-wave norm reads the row again for its sum of squares, so it issues the
+  // prefetch after that pass.
+  constexpr bool kEarlyPrefetch = !(kKind == kNorm && !kSingle);
+
+  // One token of the team: compute `cur` while the next token's row loads into `nxt`.
+  auto step = [&](Raw<kKind, T> &cur, Raw<kKind, T> &nxt) __attribute__((always_inline)) {
+    const bool live = token < args.tokens;
+    const int next = token + stride;
+    if (kEarlyPrefetch) load(nxt, next);
+    // Keep the prefetch ahead of the first use of `cur` (its wait).
+    __builtin_amdgcn_sched_barrier(0);
+
+    float rms_inv = 0.0f;
+    if (kKind == kNorm) {
+      // Sum of squares, kernels/prepare_norm_i8.loom:90-143. The reference's lane L of
+      // 256 accumulates x^2 over chunks L, L+256, ... of 8 values into 8 partials, sums
+      // them left to right, butterflies within its 32-lane wave, and adds the eight
+      // wave partials as ((p0+p4)+(p2+p6))+((p1+p5)+(p3+p7)).
+      float total;
+      if (kSingle) {
+        // Run r holds chunks 2r, 2r+1: virtual lanes (2r) mod 256 and +1, in chunk
+        // sequence t/2. Lane bits 0, 1, 3, 2 are virtual-lane bits 1, 2, 3, 4.
+        float acc[2][2][8];
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int p = 0; p < 2; ++p)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[s][p][e] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          if (!valid[t]) continue;
+#pragma unroll
+          for (int p = 0; p < 2; ++p) {
+            const v4u w = cur.x[t][p];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const uint32_t word = w[e >> 1];
+              const float xf = (e & 1) ? hi_bf16(word) : lo_bf16(word);
+              const float sq = xf * xf;
+              acc[t & 1][p][e] = acc[t & 1][p][e] + sq;
+            }
+          }
+        }
+        float u[2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          float sv[2];
+#pragma unroll
+          for (int p = 0; p < 2; ++p) {
+            float x = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x = x + acc[s][p][e];
+            sv[p] = x;
+          }
+          u[s] = sv[0] + sv[1];              // virtual stride 1
+          u[s] = u[s] + dpp<kQuadXor1>(u[s]); // virtual stride 2
+          u[s] = u[s] + dpp<kQuadXor2>(u[s]); // virtual stride 4
+          u[s] = u[s] + dpp<kRowRor8>(u[s]);  // virtual stride 8
+          u[s] = u[s] + __shfl_xor(u[s], 4);  // virtual stride 16
+        }
+        // Lane row r holds wave partials p_r (s = 0) and p_{r+4} (s = 1).
+        const float pair = u[0] + u[1];
+        const float half = pair + __shfl_xor(pair, 32);  // rows r, r^2
+        total = half + __shfl_xor(half, 16);             // rows r, r^1
+      } else {
+        // Canonical pass over the row (an L2 re-read): team thread v' takes the
+        // virtual lanes v' + 64 wpt k, which keep its position within a 32-lane wave.
+        const int tt = wave_in_team * 64 + lane;
+        const int chunks = width >> 3;
+        const uint16_t *hr = args.h + (int64_t)(live ? token : 0) * width;
+        for (int v = tt; v < 256; v += 64 * wpt) {
+          float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+          if (live) {
+            for (int c = v; c < chunks; c += 256) {
+              const v4u w = *reinterpret_cast<const v4u *>(hr + c * 8);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                const float xf = (e & 1) ? hi_bf16(w[e >> 1]) : lo_bf16(w[e >> 1]);
+                const float sq = xf * xf;
+                acc[e] = acc[e] + sq;
+              }
+            }
+          }
+          float s = 0.0f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) s = s + acc[e];
+#pragma unroll
+          for (int st = 1; st < 32; st <<= 1) s = s + __shfl_xor(s, st);
+          if ((v & 31) == 0) lds_part[iter & 1][team][v >> 5] = s;
+        }
+        __syncthreads();
+        const float *p = lds_part[iter & 1][team];
+        const float pair0 = p[0] + p[4], pair1 = p[1] + p[5];
+        const float pair2 = p[2] + p[6], pair3 = p[3] + p[7];
+        total = (pair0 + pair2) + (pair1 + pair3);
+      }
+      if (!kEarlyPrefetch) {
+        load(nxt, next);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      const float mean = total / (float)width;
+      const float mean_eps = mean + args.eps;
+      rms_inv = 1.0f / __builtin_sqrtf(mean_eps);
+    }
+
+    // Form, rotate and bound each run.
+    float v[T][16];
+    float amax = 0.0f;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      if (!valid[t]) continue;
+      if (kKind == kNorm) {
+        // kernels/prepare_norm_i8.loom:145-170
+        float ns1[16], ms1[16], shf[16];
+        factors(run0 + 64 * t, ns1, ms1, shf);
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+          const uint32_t word = cur.x[t][i >> 3][(i >> 1) & 3];
+          float n0 = lo_bf16(word) * rms_inv, n1 = hi_bf16(word) * rms_inv;
+          float a0 = n0 * ns1[i], a1 = n1 * ns1[i + 1];
+          bf16_round2(a0, a1);
+          float b0 = a0 * ms1[i], b1 = a1 * ms1[i + 1];
+          bf16_round2(b0, b1);
+          float c0 = b0 + shf[i], c1 = b1 + shf[i + 1];
+          bf16_round2(c0, c1);
+          v[t][i] = c0;
+          v[t][i + 1] = c1;
+        }
+      } else if (kKind == kPlain) {
+        // kernels/prepare_plain_i8.loom:89-90
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+          const uint32_t word = cur.x[t][i >> 3][(i >> 1) & 3];
+          v[t][i] = f16_value((uint16_t)(word & 0xffffu));
+          v[t][i + 1] = f16_value((uint16_t)(word >> 16));
+        }
+      } else {
+        // kernels/prepare_gated_i8.loom:86-108
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+          const uint32_t aw = cur.x[t][i >> 3][(i >> 1) & 3];
+          const uint32_t gw = cur.g[t][i >> 3][(i >> 1) & 3];
+          float a0 = f16_value((uint16_t)(aw & 0xffffu)), a1 = f16_value((uint16_t)(aw >> 16));
+          bf16_round2(a0, a1);
+          float s0 = sigmoid(f16_value((uint16_t)(gw & 0xffffu)));
+          float s1 = sigmoid(f16_value((uint16_t)(gw >> 16)));
+          bf16_round2(s0, s1);
+          float p0 = a0 * s0, p1 = a1 * s1;
+          bf16_round2(p0, p1);
+          v[t][i] = p0;
+          v[t][i + 1] = p1;
+        }
+      }
+      radix4_reg<1, kQuarter>(v[t]);
+      radix4_reg<4, kQuarter>(v[t]);
+      radix4_quad<kQuarter>(v[t]);
+      radix4_row<kQuarter>(v[t]);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[t][i]));
+    }
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) amax = fmaxf(amax, __shfl_xor(amax, s));
+    if (!kSingle) {
+      if (lane == 0) lds_amax[iter & 1][team][wave_in_team] = amax;
+      __syncthreads();
+      for (int w = 0; w < wpt; ++w) amax = fmaxf(amax, lds_amax[iter & 1][team][w]);
+    }
+
+    // Scale (kernels/prepare_plain_i8.loom:294-299, kernels/prepare_norm_i8.loom:322-327).
+    const float rotation_scale = kQuarter ? 16.0f : 0.0625f;
+    const float row_max = amax * rotation_scale;
+    const float safe = fmaxf(row_max, 1e-30f);
+    const float scale = safe / 127.0f;
+    const float inv = rotation_scale / scale;
+
+    // Quantise and store 16 bytes per run (:301-340, bytes low first).
+    if (live) {
+      int8_t *qr = args.q + (int64_t)token * args.out_stride;
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        if (!valid[t]) continue;
+        v4u out;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          uint32_t word = 0;
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            // clamp(rne(x), +-127) == rne(clamp(x, +-127)) as the bounds are integers
+            // (a NaN clamps to -127 either way). Adding 1.5 * 2^23 rounds to the
+            // nearest even integer, left in the low mantissa bits in two's complement.
+            float qv = v[t][4 * i + b] * inv;
+            qv = fmaxf(qv, -127.0f);
+            qv = fminf(qv, 127.0f);
+            const float biased = qv + 12582912.0f;
+            word |= (__float_as_uint(biased) & 0xffu) << (8 * b);
+          }
+          out[i] = word;
+        }
+        *reinterpret_cast<v4u *>(qr + ((run0 + 64 * t) << 4)) = out;
+      }
+      if (wave_in_team == 0 && lane == 0) args.q_scale[token] = scale;
+    }
+    token = next;
+    ++iter;
+  };
+
+  // Two row buffers in turn (no copy between iterations, so the prefetch never waits
+  // on the row being computed). Every team of the block runs the same number of
+  // steps (barriers inside).
+  Raw<kKind, T> other;
+  for (int base = blockIdx.x * teams; base < args.tokens; base += 2 * stride) {
+    step(cur, other);
+    if (base + stride >= args.tokens) break;
+    step(other, cur);
   }
-  if (lane == 0) args.q_scale[token] = scale;
+}
+
+// Device multiprocessor counts, cached per device ordinal.
+int device_cus() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Waves per CU the persistent grid aims for: enough to cover load latency while each
+// team still loops over several tokens.
+#ifndef K2W8_PREPARE_WAVES_PER_CU
+#define K2W8_PREPARE_WAVES_PER_CU 32
+#endif
+
+template <int kKind, int T, bool kSingle>
+hipError_t launch_team(hipStream_t stream, const PrepareArgs &a) {
+  const int threads = 64 * a.wpt * a.teams;
+  const int needed = (a.tokens + a.teams - 1) / a.teams;
+  int per_cu = K2W8_PREPARE_WAVES_PER_CU / (a.wpt * a.teams);
+  if (per_cu < 1) per_cu = 1;
+  const int cap = device_cus() * per_cu;
+  dim3 grid(needed < cap ? needed : cap), block(threads);
+  const size_t lds = (kKind == kNorm && kSingle) ? (size_t)a.width * 12 : 0;
+  hipLaunchKernelGGL((prepare_kernel<kKind, T, kSingle>), grid, block, lds, stream, a);
+  return hipGetLastError();
+}
+
+#ifndef K2W8_PREPARE_MAX_RUNS_PER_LANE
+#define K2W8_PREPARE_MAX_RUNS_PER_LANE 1
+#endif
+
+// Team shape for a row: the fewest waves (at most 16) that hold it with at most
+// `max_runs` runs of 16 elements per lane; single-wave teams are packed four to a
+// block and two-wave teams two to a block.
+void team_shape(PrepareArgs &a, int max_runs, int &t) {
+  const int runs = a.width >> 4;
+  int wpt = (runs + 64 * max_runs - 1) / (64 * max_runs);
+  if (wpt > kMaxWpt) wpt = kMaxWpt;
+  t = (runs + 64 * wpt - 1) / (64 * wpt);
+  if (t > 2 && wpt > 8) {  // more than 8 waves of three or four runs: use two runs
+    t = 2;
+    wpt = (runs + 127) / 128;
+  }
+  a.wpt = wpt;
+  a.teams = wpt == 1 ? kMaxTeams : (wpt == 2 ? 2 : 1);
+}
+
+template <int kKind, bool kSingle>
+hipError_t launch_t(int t, hipStream_t stream, const PrepareArgs &a) {
+  switch (t) {
+    case 1: return launch_team<kKind, 1, kSingle>(stream, a);
+    case 2: return launch_team<kKind, 2, kSingle>(stream, a);
+    case 3: return launch_team<kKind, 3, kSingle>(stream, a);
+    default: return launch_team<kKind, 4, kSingle>(stream, a);
+  }
+}
+
+template <int kKind>
+hipError_t launch_kind(hipStream_t stream, PrepareArgs a) {
+  // The norm keeps rows of up to 4096 in one wave (sum of squares from registers,
+  // factors in LDS); the other prepares use K2W8_PREPARE_MAX_RUNS_PER_LANE.
+  int t = 1;
+  team_shape(a, kKind == kNorm ? 4 : K2W8_PREPARE_MAX_RUNS_PER_LANE, t);
+  if (a.wpt == 1) return launch_t<kKind, true>(t, stream, a);
+  return launch_t<kKind, false>(t, stream, a);
 }
 
 }  // namespace
@@ -256,37 +546,19 @@ hipError_t launch_prepare(int kind, hipStream_t stream, int64_t tokens, const Pr
   a.mod_shift = p.mod_shift;
   a.q = p.q;
   a.q_scale = p.q_scale;
+  a.tokens = (int)tokens;
   a.width = (int)p.width;
   a.out_stride = (int)p.out_stride;
   a.gate_stride = (int)p.gate_stride;
   a.eps = p.eps;
-  const size_t lds = (size_t)(p.width + (p.width >> 6) * 4) * sizeof(float);
-  dim3 grid((unsigned)tokens), block(kThreads);
   switch (kind) {
-    case kNorm:
-      hipLaunchKernelGGL(prepare_kernel<kNorm>, grid, block, lds, stream, a);
-      break;
-    case kPlain:
-      hipLaunchKernelGGL(prepare_kernel<kPlain>, grid, block, lds, stream, a);
-      break;
-    default:
-      hipLaunchKernelGGL(prepare_kernel<kGated>, grid, block, lds, stream, a);
-      break;
+    case kNorm: return launch_kind<kNorm>(stream, a);
+    case kPlain: return launch_kind<kPlain>(stream, a);
+    default: return launch_kind<kGated>(stream, a);
   }
-  return hipGetLastError();
 }
 
-hipError_t configure_prepare_lds() {
-  // The widest row, 32768 f32 values plus four floats of padding per 64.
-  const int max_lds = (32768 + (32768 >> 6) * 4) * (int)sizeof(float);
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(prepare_kernel<kNorm>),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
-  if (e != hipSuccess) return e;
-  e = hipFuncSetAttribute(reinterpret_cast<const void *>(prepare_kernel<kPlain>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
-  if (e != hipSuccess) return e;
-  return hipFuncSetAttribute(reinterpret_cast<const void *>(prepare_kernel<kGated>),
-                             hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
-}
+// The prepares use static LDS only.
+hipError_t configure_prepare_lds() { return hipSuccess; }
 
 }  // namespace k2w8
