@@ -130,12 +130,18 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, v16i (&acc)[FM][FN
           const float us[4] = {wu[q].x, wu[q].y, wu[q].z, wu[q].w};
           uint32_t packed[2];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float gv = bf16_round(((float)acc[i][j][4 * q + r] * gs[r]) * as[i]);
-            const float uv = bf16_round(((float)acc[i][j][8 + 4 * q + r] * us[r]) * as[i]);
-            const float silu = bf16_round(gv * sigmoid(gv));
-            const uint32_t h = f16_bits(bf16_round(silu * uv));
-            if (r & 1) packed[r >> 1] |= h << 16; else packed[r >> 1] = h;
+          for (int r = 0; r < 4; r += 2) {
+            float g0 = ((float)acc[i][j][4 * q + r] * gs[r]) * as[i];
+            float g1 = ((float)acc[i][j][4 * q + r + 1] * gs[r + 1]) * as[i];
+            float u0 = ((float)acc[i][j][8 + 4 * q + r] * us[r]) * as[i];
+            float u1 = ((float)acc[i][j][8 + 4 * q + r + 1] * us[r + 1]) * as[i];
+            bf16_round2(g0, g1);
+            bf16_round2(u0, u1);
+            float s0 = g0 * sigmoid(g0), s1 = g1 * sigmoid(g1);
+            bf16_round2(s0, s1);
+            float p0 = s0 * u0, p1 = s1 * u1;
+            bf16_round2(p0, p1);
+            packed[r >> 1] = f16_pack2(p0, p1);
           }
           *reinterpret_cast<uint2 *>(out + 8 * q) = make_uint2(packed[0], packed[1]);
         }
@@ -178,20 +184,24 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, v16i (&acc)[FM][FN
         const uint32_t pw[2] = {prior.x, prior.y};
         uint32_t packed[2];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        for (int r = 0; r < 4; r += 2) {
           const int e = 4 * q + r;
-          const float v = ((float)acc[i][j][e] * ws[e]) * as[i];
-          uint32_t h;
-          if (EPI == kEpiPlain) {
-            h = f16_bits(bf16_round(v));
-          } else if (EPI == kEpiBias) {
-            h = f16_bits(bf16_round(v + extra[e]));
-          } else {  // residual: x = bf16(x + bf16(gate * bf16(v)))
-            const float gated = bf16_round(bf16_round(v) * extra[e]);
-            const float x = bf16_value((uint16_t)((r & 1) ? (pw[r >> 1] >> 16) : (pw[r >> 1] & 0xffffu)));
-            h = bf16_bits(x + gated);
+          float v0 = ((float)acc[i][j][e] * ws[e]) * as[i];
+          float v1 = ((float)acc[i][j][e + 1] * ws[e + 1]) * as[i];
+          if (EPI == kEpiBias) {
+            v0 = v0 + extra[e];
+            v1 = v1 + extra[e + 1];
           }
-          if (r & 1) packed[r >> 1] |= h << 16; else packed[r >> 1] = h;
+          bf16_round2(v0, v1);
+          if (EPI == kEpiResid) {  // x = bf16(x + bf16(gate * bf16(v)))
+            float g0 = v0 * extra[e], g1 = v1 * extra[e + 1];
+            bf16_round2(g0, g1);
+            const uint32_t w = pw[r >> 1];
+            packed[r >> 1] = bf16_pack2(__uint_as_float(w << 16) + g0,
+                                        __uint_as_float(w & 0xffff0000u) + g1);
+          } else {
+            packed[r >> 1] = f16_pack2(v0, v1);
+          }
         }
         *reinterpret_cast<uint2 *>(out + 8 * q) = make_uint2(packed[0], packed[1]);
       }

@@ -25,6 +25,28 @@ __device__ __forceinline__ float bf16_value(uint16_t b) {
   return __uint_as_float((uint32_t)b << 16);
 }
 
+typedef float k2w8_f2 __attribute__((ext_vector_type(2)));
+typedef __bf16 k2w8_bf2 __attribute__((ext_vector_type(2)));
+typedef _Float16 k2w8_h2 __attribute__((ext_vector_type(2)));
+
+// Two f32 values to packed bf16 (low half first) with the hardware conversion,
+// round to nearest even: the same bits as bf16_bits for every non-NaN input.
+__device__ __forceinline__ uint32_t bf16_pack2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(k2w8_f2{a, b}, k2w8_bf2));
+}
+
+// Two values rounded to bf16 and widened back to f32 (bf16_round on each).
+__device__ __forceinline__ void bf16_round2(float &a, float &b) {
+  const uint32_t u = bf16_pack2(a, b);
+  a = __uint_as_float(u << 16);
+  b = __uint_as_float(u & 0xffff0000u);
+}
+
+// Two f32 values to packed f16 (low half first), round to nearest even.
+__device__ __forceinline__ uint32_t f16_pack2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(k2w8_f2{a, b}, k2w8_h2));
+}
+
 // f32 -> f16 (hardware conversion, round to nearest even) and back.
 __device__ __forceinline__ uint16_t f16_bits(float x) {
   _Float16 h = (_Float16)x;

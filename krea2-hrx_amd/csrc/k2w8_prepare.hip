@@ -44,8 +44,6 @@ namespace {
 enum PrepareKind { kNorm = 0, kPlain = 1, kGated = 2 };
 
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
-typedef float f2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
 
 // DPP controls: quad_perm [1,0,3,2], [2,3,0,1]; row_ror by 8.
 constexpr int kQuadXor1 = 0xB1, kQuadXor2 = 0x4E, kRowRor8 = 0x128;
@@ -54,15 +52,6 @@ template <int kCtrl>
 __device__ __forceinline__ float dpp(float x) {
   return __builtin_bit_cast(
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kCtrl, 0xf, 0xf, true));
-}
-
-// Two values rounded to bf16 (round to nearest even, the hardware conversion) and
-// widened back to f32. Identical to the bit-pattern rounding of src/numerics.rs:18-26
-// for every non-NaN input.
-__device__ __forceinline__ void bf16_round2(float &a, float &b) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, bf2));
-  a = __uint_as_float(u << 16);
-  b = __uint_as_float(u & 0xffff0000u);
 }
 
 __device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }

@@ -52,12 +52,17 @@ __device__ __forceinline__ void store_block(const Args &g, const v4i (&acc)[RB /
     const float gsv[4] = {gs.x, gs.y, gs.z, gs.w}, usv[4] = {us.x, us.y, us.z, us.w};
     uint32_t packed[2];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float gv = bf16_round(((float)acc[0][e] * gsv[e]) * as);
-      const float uv = bf16_round(((float)acc[RB / 16 - 1][e] * usv[e]) * as);
-      const float silu = bf16_round(gv * sigmoid(gv));
-      const uint32_t h = f16_bits(bf16_round(silu * uv));
-      if (e & 1) packed[e >> 1] |= h << 16; else packed[e >> 1] = h;
+    for (int e = 0; e < 4; e += 2) {
+      float g0 = ((float)acc[0][e] * gsv[e]) * as, g1 = ((float)acc[0][e + 1] * gsv[e + 1]) * as;
+      float u0 = ((float)acc[RB / 16 - 1][e] * usv[e]) * as;
+      float u1 = ((float)acc[RB / 16 - 1][e + 1] * usv[e + 1]) * as;
+      bf16_round2(g0, g1);
+      bf16_round2(u0, u1);
+      float s0 = g0 * sigmoid(g0), s1 = g1 * sigmoid(g1);
+      bf16_round2(s0, s1);
+      float p0 = s0 * u0, p1 = s1 * u1;
+      bf16_round2(p0, p1);
+      packed[e >> 1] = f16_pack2(p0, p1);
     }
     uint16_t *out = static_cast<uint16_t *>(g.c) + (int64_t)tok * (g.n >> 1) + (n0 >> 1) + 4 * kq;
     *reinterpret_cast<uint2 *>(out) = make_uint2(packed[0], packed[1]);
@@ -88,19 +93,21 @@ __device__ __forceinline__ void store_block(const Args &g, const v4i (&acc)[RB /
     const uint32_t pw[2] = {prior.x, prior.y};
     uint32_t packed[2];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float v = ((float)acc[rb][e] * ws[e]) * as;
-      uint32_t h;
-      if (EPI == kEpiPlain) {
-        h = f16_bits(bf16_round(v));
-      } else if (EPI == kEpiBias) {
-        h = f16_bits(bf16_round(v + extra[e]));
-      } else {
-        const float gated = bf16_round(bf16_round(v) * extra[e]);
-        const float x = bf16_value((uint16_t)((e & 1) ? (pw[e >> 1] >> 16) : (pw[e >> 1] & 0xffffu)));
-        h = bf16_bits(x + gated);
+    for (int e = 0; e < 4; e += 2) {
+      float v0 = ((float)acc[rb][e] * ws[e]) * as, v1 = ((float)acc[rb][e + 1] * ws[e + 1]) * as;
+      if (EPI == kEpiBias) {
+        v0 = v0 + extra[e];
+        v1 = v1 + extra[e + 1];
       }
-      if (e & 1) packed[e >> 1] |= h << 16; else packed[e >> 1] = h;
+      bf16_round2(v0, v1);
+      if (EPI == kEpiResid) {  // x = bf16(x + bf16(gate * bf16(v)))
+        float g0 = v0 * extra[e], g1 = v1 * extra[e + 1];
+        bf16_round2(g0, g1);
+        const uint32_t w = pw[e >> 1];
+        packed[e >> 1] = bf16_pack2(__uint_as_float(w << 16) + g0, __uint_as_float(w & 0xffff0000u) + g1);
+      } else {
+        packed[e >> 1] = f16_pack2(v0, v1);
+      }
     }
     *reinterpret_cast<uint2 *>(out) = make_uint2(packed[0], packed[1]);
   }
