@@ -17,77 +17,13 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "k2w8_gemm_common.hpp"
 #include "k2w8_internal.hpp"
 #include "k2w8_numerics.hpp"
 
 namespace k2w8 {
 
 namespace gemm {
-
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
-
-constexpr int kXcds = 8;  // MI355X: 8 XCDs, workgroups dispatched round-robin
-
-struct GemmArgs {
-  const int8_t *a, *w;
-  const float *w_scale, *a_scale;
-  void *c;
-  const float *gate;
-  const uint16_t *bias;
-  int m, n, k, lda, m_group;
-};
-
-#ifndef K2W8_SWZ_SHIFT
-#define K2W8_SWZ_SHIFT 1
-#endif
-
-// Staged operand rows are BK bytes = BK/16 chunks of 16 bytes. The chunk index is
-// XORed with bits of the row so that the consecutive rows one LDS cycle serves (one
-// chunk each) land on distinct banks.
-template <int BK>
-__device__ __forceinline__ int swz_key(int r) {
-  return (r >> K2W8_SWZ_SHIFT) & (BK / 16 - 1);
-}
-
-// One 16-byte-per-lane global -> LDS transfer (global_load_lds_dwordx4): lane l
-// writes LDS bytes [lds + 16 l, lds + 16 l + 16) from global address base + voff.
-// Issued through asm so that the waits for it are placed by hand (the compiler
-// would otherwise wait for every transfer in flight before any LDS read).
-__device__ __forceinline__ void dma16(uint32_t lds, const int8_t *base, uint32_t voff) {
-  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds) : "memory");
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// Tile of workgroup `bid`: XCD-major renumbering, then m_group m-tiles per n sweep.
-__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int m_group, int &tm,
-                                        int &tn) {
-  const int total = tiles_m * tiles_n;
-  const int per_xcd = total / kXcds;
-  if (bid < per_xcd * kXcds) bid = (bid % kXcds) * per_xcd + bid / kXcds;
-  const int span = m_group * tiles_n;
-  const int group = bid / span, in_group = bid - group * span;
-  const int first_m = group * m_group;
-  const int rows_in_group = min(tiles_m - first_m, m_group);
-  tm = first_m + in_group % rows_in_group;
-  tn = in_group / rows_in_group;
-}
-
-// This wave's A and B fragments of one 32-byte K slice: LDS chunk offset `c` of each
-// fragment row.
-template <int FM, int FN>
-__device__ __forceinline__ void read_frags(v4i (&af)[FM], v4i (&bf)[FN], const uint8_t *stage,
-                                           const int (&a_row_off)[FM], const int (&b_row_off)[FN],
-                                           int c) {
-#pragma unroll
-  for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const v4i *>(stage + a_row_off[i] + c);
-#pragma unroll
-  for (int j = 0; j < FN; ++j) bf[j] = *reinterpret_cast<const v4i *>(stage + b_row_off[j] + c);
-}
 
 // Epilogue of one wave's (32 FM) x (32 FN) sub-tile at rows m_base.., columns n_base..
 template <int EPI, int FM, int FN>
@@ -403,12 +339,35 @@ inline GemmArgs args_of(const GemmLaunch &l) {
 }  // namespace gemm
 
 #ifndef K2W8_GEMM_NO_ENTRY
+// Wave grids of the 256-row tiles (waves along M x along N).
+#ifndef K2W8_BIG_WM
+#define K2W8_BIG_WM 4
+#endif
+#ifndef K2W8_MID_WM
+#define K2W8_MID_WM 4
+#endif
+constexpr int kBigWm = K2W8_BIG_WM, kBigWn = 8 / kBigWm;
+constexpr int kMidWm = K2W8_MID_WM, kMidWn = 8 / kMidWm;
+
+int device_cus() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 // Token counts served by the few-token kernel (weights streamed, HBM-bound).
 constexpr int64_t kSkinnyMaxTokens = 128;
 
 hipError_t configure_gemm_lds() {
-  hipError_t e = gemm::set_lds_tile<256, 256, 4, 2, 128, 2>();
-  if (e == hipSuccess) e = gemm::set_lds_tile<256, 128, 4, 2, 128, 2>();
+  hipError_t e = gemm::set_lds_tile<256, 256, kBigWm, kBigWn, 128, 2>();
+  if (e == hipSuccess) e = gemm::set_lds_tile<256, 128, kMidWm, kMidWn, 128, 2>();
   if (e == hipSuccess) e = gemm::set_lds_tile<128, 128, 2, 2, 128, 2>();
   if (e == hipSuccess) e = gemm::set_lds_tile<64, 64, 2, 2, 128, 2>();
   return e;
@@ -420,10 +379,11 @@ hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &l) {
   if (l.m <= kSkinnyMaxTokens) return launch_skinny(epilogue, stream, l);
   const gemm::GemmArgs a = gemm::args_of(l);
   auto tiles = [&](int64_t bm, int64_t bn) { return ((l.m + bm - 1) / bm) * (l.n / bn); };
-  constexpr int64_t kCus = 256;
+  const int64_t kCus = device_cus();
   if (l.n % 256 == 0 && tiles(256, 256) >= kCus)
-    return gemm::launch_tile<256, 256, 4, 2, 128, 2>(epilogue, stream, a);
-  if (tiles(256, 128) >= kCus) return gemm::launch_tile<256, 128, 4, 2, 128, 2>(epilogue, stream, a);
+    return gemm::launch_tile<256, 256, kBigWm, kBigWn, 128, 2>(epilogue, stream, a);
+  if (tiles(256, 128) >= kCus)
+    return gemm::launch_tile<256, 128, kMidWm, kMidWn, 128, 2>(epilogue, stream, a);
   if (tiles(128, 128) >= kCus) return gemm::launch_tile<128, 128, 2, 2, 128, 2>(epilogue, stream, a);
   return gemm::launch_tile<64, 64, 2, 2, 128, 2>(epilogue, stream, a);
 }

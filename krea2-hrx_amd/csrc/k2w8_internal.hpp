@@ -37,4 +37,7 @@ hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &g);
 hipError_t launch_skinny(int epilogue, hipStream_t stream, const GemmLaunch &g);
 hipError_t configure_gemm_lds();
 
+// Multiprocessor (CU) count of the current device, cached per device ordinal.
+int device_cus();
+
 }  // namespace k2w8

@@ -451,20 +451,6 @@ __global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArg
   }
 }
 
-// Device multiprocessor counts, cached per device ordinal.
-int device_cus() {
-  static int cached[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
 // Waves per CU the persistent grid aims for: enough to cover load latency while each
 // team still loops over several tokens.
 #ifndef K2W8_PREPARE_WAVES_PER_CU
