@@ -159,6 +159,38 @@ int k2w8_gemm_i8_bias(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, const i
 int k2w8_gemm_i8_acc(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, const int8_t *a,
                      const int8_t *w, int32_t *acc);
 
+/*
+ * lora_transport: replaces krea2_lora_transport (kernels/native/lora_transport.loom:5-41),
+ * the 16-bit format change around the W8A8 projection of src/training/quantized.rs:66-105.
+ * Each element is widened exactly to f32 and rounded (nearest even) to the other format.
+ *   direction 1 (the reference's `reverse` = 1): x bf16 [count] -> out f16 [count]
+ *   direction 2 (`reverse` = 2):                 x f16 [count]  -> out bf16 [count]
+ * count in 1..2^30-1 (:13); x and out 16-byte aligned.
+ */
+int k2w8_lora_transport(void *stream, int direction, int64_t count, const void *x, void *out);
+
+/* Shape of a ConvRot projection (src/training/quantized.rs:8-14). */
+typedef struct k2w8_quantized_cfg {
+  int64_t inputs;  /* K: a multiple of 256 (prepare width rules) */
+  int64_t outputs; /* N: a multiple of 128 */
+  int64_t pitch;   /* row pitch of weight and quantized rows (k2w8_shape_gemm_pitch(inputs)) */
+} k2w8_quantized_cfg;
+
+/*
+ * quantized_forward: Quantized::forward (src/training/quantized.rs:51-112), the
+ * secondary caller of the path, as one call issuing its four launches in order on
+ * `stream`: transport bf16 -> f16, prepare_plain_i8, gemm_i8, transport f16 -> bf16.
+ * The caller owns every buffer, including the workspaces the reference takes from its
+ * pool (:55-58):
+ *   x bf16 [rows][inputs], weight int8 [outputs][pitch], scales f32 [outputs],
+ *   transport f16 [rows * inputs], quantized int8 [rows][pitch], q_scales f32 [rows],
+ *   out_f16 f16 [rows][outputs], out bf16 [rows][outputs].
+ */
+int k2w8_quantized_forward(void *stream, const k2w8_quantized_cfg *cfg, int64_t rows,
+                           const void *x, const int8_t *weight, const float *scales,
+                           void *transport, int8_t *quantized, float *q_scales, void *out_f16,
+                           void *out);
+
 /* Launch-shape rules of src/kernels/shape.rs:7-112. */
 int64_t k2w8_shape_gemm_pitch(int64_t k);    /* shape.rs:105-107 */
 int64_t k2w8_shape_capacity(int64_t tokens); /* shape.rs:12-16 */

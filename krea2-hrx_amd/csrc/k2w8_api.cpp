@@ -254,6 +254,45 @@ int k2w8_gemm_i8_acc(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, const in
                   nullptr, nullptr);
 }
 
+int k2w8_lora_transport(void *stream, int direction, int64_t count, const void *x, void *out) {
+  const char *stage = "lora_transport";
+  if (direction != 1 && direction != 2)
+    return fail(K2W8_INVALID_ARGUMENT, "%s: direction must be 1 (bf16 -> f16) or 2 (f16 -> bf16), got %d",
+                stage, direction);
+  // kernels/native/lora_transport.loom:13
+  if (count < 1 || count >= (int64_t(1) << 30))
+    return fail(K2W8_INVALID_ARGUMENT, "%s: count must be 1..2^30-1, got %lld", stage,
+                (long long)count);
+  if (!x || !out) return fail(K2W8_INVALID_ARGUMENT, "%s: null buffer", stage);
+  if (!aligned(x, 16) || !aligned(out, 16))
+    return fail(K2W8_INVALID_ARGUMENT, "%s: x and out must be 16-byte aligned", stage);
+  hipError_t e = k2w8::launch_transport(direction, static_cast<hipStream_t>(stream), count, x, out);
+  if (e != hipSuccess) return runtime(stage, e);
+  return ok();
+}
+
+// src/training/quantized.rs:51-112
+int k2w8_quantized_forward(void *stream, const k2w8_quantized_cfg *cfg, int64_t rows,
+                           const void *x, const int8_t *weight, const float *scales,
+                           void *transport, int8_t *quantized, float *q_scales, void *out_f16,
+                           void *out) {
+  const char *stage = "quantized_forward";
+  if (!cfg) return fail(K2W8_INVALID_ARGUMENT, "%s: null configuration", stage);
+  if (rows < 1 || rows * cfg->inputs >= (int64_t(1) << 30) ||
+      rows * cfg->outputs >= (int64_t(1) << 30))
+    return fail(K2W8_INVALID_ARGUMENT, "%s: rows * inputs and rows * outputs must be below 2^30",
+                stage);
+  int rc = k2w8_lora_transport(stream, 1, rows * cfg->inputs, x, transport);
+  if (rc != K2W8_OK) return rc;
+  const k2w8_prepare_plain_cfg prep = {cfg->inputs, cfg->pitch};
+  rc = k2w8_prepare_plain_i8(stream, &prep, rows, transport, quantized, q_scales);
+  if (rc != K2W8_OK) return rc;
+  const k2w8_gemm_cfg gemm = {cfg->inputs, cfg->outputs, cfg->pitch, k2w8_shape_gemm_m_group(), 0};
+  rc = k2w8_gemm_i8(stream, &gemm, rows, quantized, weight, scales, q_scales, out_f16);
+  if (rc != K2W8_OK) return rc;
+  return k2w8_lora_transport(stream, 2, rows * cfg->outputs, out_f16, out);
+}
+
 // src/kernels/shape.rs:105-107
 int64_t k2w8_shape_gemm_pitch(int64_t k) { return (k % 8192 == 0) ? k + 64 : k; }
 

@@ -37,6 +37,10 @@ hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &g);
 hipError_t launch_skinny(int epilogue, hipStream_t stream, const GemmLaunch &g);
 hipError_t configure_gemm_lds();
 
+// bf16 <-> f16 transport: direction 1 bf16 -> f16, 2 f16 -> bf16.
+hipError_t launch_transport(int direction, hipStream_t stream, int64_t count, const void *x,
+                            void *out);
+
 // Multiprocessor (CU) count of the current device, cached per device ordinal.
 int device_cus();
 

@@ -16,12 +16,14 @@ from . import shape  # noqa: F401  (re-exported)
 from ._lib import Internal, InvalidArgument, Krea2Error, Runtime, lib, library_path  # noqa: F401
 from .ops import (  # noqa: F401
     GemmConfig,
+    Quantized,
     gemm_i8,
     gemm_i8_acc,
     gemm_i8_bias,
     gemm_i8_resid,
     gemm_i8_resid_256x256,
     gemm_i8_swiglu,
+    lora_transport,
     prepare_gated_i8,
     prepare_norm_i8,
     prepare_plain_i8,
@@ -32,6 +34,7 @@ __all__ = [
     "Internal",
     "InvalidArgument",
     "Krea2Error",
+    "Quantized",
     "Runtime",
     "gemm_i8",
     "gemm_i8_acc",
@@ -41,6 +44,7 @@ __all__ = [
     "gemm_i8_swiglu",
     "lib",
     "library_path",
+    "lora_transport",
     "prepare_gated_i8",
     "prepare_norm_i8",
     "prepare_plain_i8",

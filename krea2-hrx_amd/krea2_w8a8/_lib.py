@@ -51,6 +51,10 @@ class PrepareGatedCfg(ctypes.Structure):
     ]
 
 
+class QuantizedCfg(ctypes.Structure):
+    _fields_ = [("inputs", ctypes.c_int64), ("outputs", ctypes.c_int64), ("pitch", ctypes.c_int64)]
+
+
 class GemmCfg(ctypes.Structure):
     _fields_ = [
         ("k_size", ctypes.c_int64),
@@ -86,6 +90,11 @@ SIGNATURES = {
     "k2w8_gemm_i8_swiglu": (ctypes.c_int, [_P, ctypes.POINTER(GemmCfg), _I64, _P, _P, _P, _P, _P]),
     "k2w8_gemm_i8_bias": (ctypes.c_int, [_P, ctypes.POINTER(GemmCfg), _I64, _P, _P, _P, _P, _P, _P]),
     "k2w8_gemm_i8_acc": (ctypes.c_int, [_P, ctypes.POINTER(GemmCfg), _I64, _P, _P, _P]),
+    "k2w8_lora_transport": (ctypes.c_int, [_P, ctypes.c_int, _I64, _P, _P]),
+    "k2w8_quantized_forward": (
+        ctypes.c_int,
+        [_P, ctypes.POINTER(QuantizedCfg), _I64, _P, _P, _P, _P, _P, _P, _P, _P],
+    ),
     "k2w8_shape_gemm_pitch": (_I64, [_I64]),
     "k2w8_shape_capacity": (_I64, [_I64]),
     "k2w8_shape_gemm_grid_rows": (_I64, [_I64]),

@@ -26,6 +26,7 @@ from ._lib import (
     PrepareGatedCfg,
     PrepareNormCfg,
     PreparePlainCfg,
+    QuantizedCfg,
     check,
     lib,
 )
@@ -180,3 +181,63 @@ def gemm_i8_acc(a, w, acc, *, cfg: GemmConfig, m=None, stream=None):
     out = _buf(acc, "acc", torch.int32, m * cfg.n_size)
     k = cfg.c()
     check(lib().k2w8_gemm_i8_acc(_stream(stream), ctypes.byref(k), m, pa, pw, out))
+
+
+def lora_transport(x, out, *, reverse: int, count=None, stream=None):
+    """The 16-bit format change of kernels/native/lora_transport.loom: ``reverse`` 1 turns
+    bf16 ``x`` into f16 ``out``, 2 turns f16 into bf16 (round to nearest even)."""
+    src, dst = (torch.bfloat16, torch.float16) if reverse == 1 else (torch.float16, torch.bfloat16)
+    n = int(x.numel()) if count is None else int(count)
+    px = _buf(x, "x", src, n)
+    po = _buf(out, "out", dst, n)
+    check(lib().k2w8_lora_transport(_stream(stream), int(reverse), n, px, po))
+
+
+@dataclass(frozen=True)
+class Quantized:
+    """A ConvRot projection on the device (src/training/quantized.rs:8-49): int8 weight
+    rows at ``pitch`` = ``shape.gemm_pitch(inputs)`` and their f32 scales."""
+
+    weight: torch.Tensor  # int8 [outputs][pitch]
+    scales: torch.Tensor  # f32 [outputs]
+    inputs: int
+    outputs: int
+
+    @property
+    def pitch(self) -> int:
+        return int(lib().k2w8_shape_gemm_pitch(self.inputs))
+
+    @staticmethod
+    def load(weight_rows: torch.Tensor, scales: torch.Tensor) -> "Quantized":
+        """Upload int8 [outputs][inputs] rows and f32 [outputs] scales at the GEMM pitch
+        (:17-49): the padding past each row stays zero."""
+        outputs, inputs = int(weight_rows.shape[0]), int(weight_rows.shape[1])
+        pitch = int(lib().k2w8_shape_gemm_pitch(inputs))
+        w = torch.zeros((outputs, pitch), dtype=torch.int8, device="cuda")
+        w[:, :inputs].copy_(weight_rows)
+        s = scales.to(device="cuda", dtype=torch.float32).contiguous()
+        return Quantized(w, s, inputs, outputs)
+
+    def forward(self, x: torch.Tensor, stream=None) -> torch.Tensor:
+        """bf16 [rows][inputs] -> bf16 [rows][outputs] (:51-112), workspaces from torch."""
+        if x.dim() != 2 or int(x.shape[1]) != self.inputs:
+            raise InvalidArgument("ConvRot projection dimensions")
+        rows = int(x.shape[0])
+        transport = torch.empty(rows * self.inputs, dtype=torch.float16, device="cuda")
+        quantized = torch.empty((rows, self.pitch), dtype=torch.int8, device="cuda")
+        q_scales = torch.empty(rows, dtype=torch.float32, device="cuda")
+        out_f16 = torch.empty((rows, self.outputs), dtype=torch.float16, device="cuda")
+        out = torch.empty((rows, self.outputs), dtype=torch.bfloat16, device="cuda")
+        cfg = QuantizedCfg(self.inputs, self.outputs, self.pitch)
+        args = (
+            _buf(x, "x", torch.bfloat16, rows * self.inputs),
+            _buf(self.weight, "weight", torch.int8, (self.outputs - 1) * self.pitch + self.inputs),
+            _buf(self.scales, "scales", torch.float32, self.outputs),
+            _buf(transport, "transport", torch.float16, rows * self.inputs),
+            _buf(quantized, "quantized", torch.int8, (rows - 1) * self.pitch + self.inputs),
+            _buf(q_scales, "q_scales", torch.float32, rows),
+            _buf(out_f16, "out_f16", torch.float16, rows * self.outputs),
+            _buf(out, "out", torch.bfloat16, rows * self.outputs),
+        )
+        check(lib().k2w8_quantized_forward(_stream(stream), ctypes.byref(cfg), rows, *args))
+        return out

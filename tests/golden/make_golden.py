@@ -199,7 +199,7 @@ def convrot_kat(inputs: int) -> dict:
         dot = wm @ codes.astype(np.int64)
         base[t] = bf16_bits_from_f32((dot.astype(np.float32) * scales) * scale)
     return dict(inputs=inputs, tokens=tokens, outputs=outputs, weights=weights, scales=scales,
-                h=h.view(np.uint16), base_bf16=base)
+                x_bf16=x, h=h.view(np.uint16), base_bf16=base)
 
 
 def main() -> None:
