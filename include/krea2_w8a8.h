@@ -191,6 +191,75 @@ int k2w8_quantized_forward(void *stream, const k2w8_quantized_cfg *cfg, int64_t 
                            void *transport, int8_t *quantized, float *q_scales, void *out_f16,
                            void *out);
 
+/* ---- Checkpoint upload (host code; src/checkpoint/, src/session/weights.rs) ---- */
+
+/* Tensor element types of a .safetensors header. */
+enum {
+  K2W8_DTYPE_OTHER = 0,
+  K2W8_DTYPE_I8 = 1,
+  K2W8_DTYPE_F32 = 2,
+  K2W8_DTYPE_BF16 = 3,
+  K2W8_DTYPE_F16 = 4,
+  K2W8_DTYPE_U8 = 5,
+  K2W8_DTYPE_I32 = 6
+};
+
+/* A memory-mapped .safetensors file, indexed under its tensors' names with a
+ * whole-model save's shared prefix removed (src/checkpoint/file.rs:64-130). */
+typedef struct k2w8_checkpoint k2w8_checkpoint;
+
+/* One tensor of a checkpoint (file.rs:12-21): its bytes point into the mapping and
+ * live as long as the checkpoint. */
+typedef struct k2w8_tensor {
+  int32_t dtype; /* K2W8_DTYPE_* */
+  int32_t ndim;
+  int64_t shape[8];
+  const void *data;
+  int64_t nbytes;
+} k2w8_tensor;
+
+/* Checkpoint::open (file.rs:86-106): a name not ending in .safetensors, a header longer
+ * than the file, or a tensor reaching past the data is INVALID_ARGUMENT. */
+int k2w8_checkpoint_open(const char *path, k2w8_checkpoint **out);
+void k2w8_checkpoint_close(k2w8_checkpoint *file);
+/* Checkpoint::block_count (file.rs:124-129). */
+int64_t k2w8_checkpoint_block_count(const k2w8_checkpoint *file);
+/* Checkpoint::get (file.rs:114-120); a missing name is INVALID_ARGUMENT. */
+int k2w8_checkpoint_tensor(const k2w8_checkpoint *file, const char *name, k2w8_tensor *out);
+
+/* The device layout of a checkpoint's ConvRot block weights (src/checkpoint/plan.rs). */
+typedef struct k2w8_plan k2w8_plan;
+
+/* One destination of the plan (plan.rs:24-41). */
+typedef struct k2w8_span {
+  int64_t device_offset;    /* in the single weights allocation, 256-byte aligned */
+  int64_t device_bytes;     /* bytes it occupies at the device pitch */
+  int64_t rows;             /* rows copied from the file (0: bytes assembled on the host) */
+  int64_t row_bytes;        /* bytes per row in the file */
+  int64_t device_row_bytes; /* bytes per row on the device (the GEMM pitch) */
+  int64_t file_bytes;       /* Span::file_bytes (plan.rs:43-48) */
+  int64_t segments;         /* checkpoint row ranges that fill it */
+} k2w8_span;
+
+/* Plan::for_checkpoint (plan.rs:88-143): per block, qkvg.{q,s} = wq|wk|wv|attn.gate rows
+ * and scales, wo.{q,s}, down.{q,s}, gu.{q,s} = mlp.gate and mlp.up interleaved 16 rows at
+ * a time, and the f32 vectors prenorm, postnorm, qnorm, knorm (bf16 upcast exactly). */
+int k2w8_plan_for_checkpoint(const k2w8_checkpoint *file, k2w8_plan **out);
+void k2w8_plan_free(k2w8_plan *plan);
+int64_t k2w8_plan_total_bytes(const k2w8_plan *plan);
+int64_t k2w8_plan_layers(const k2w8_plan *plan);
+/* The spans in name order (the order their offsets were assigned in). */
+int64_t k2w8_plan_span_count(const k2w8_plan *plan);
+const char *k2w8_plan_span_name(const k2w8_plan *plan, int64_t index);
+/* Plan::span (plan.rs:146-149); an unknown name is INVALID_ARGUMENT. */
+int k2w8_plan_span(const k2w8_plan *plan, const char *name, k2w8_span *out);
+
+/* Weights::upload (src/session/weights.rs:48-100): zero `device` (at least
+ * k2w8_plan_total_bytes bytes), then place every span's rows at its device pitch from
+ * the mapped file, on `stream`; returns after the stream has drained. */
+int k2w8_plan_upload(void *stream, const k2w8_plan *plan, const k2w8_checkpoint *file,
+                     void *device, int64_t device_bytes);
+
 /* Launch-shape rules of src/kernels/shape.rs:7-112. */
 int64_t k2w8_shape_gemm_pitch(int64_t k);    /* shape.rs:105-107 */
 int64_t k2w8_shape_capacity(int64_t tokens); /* shape.rs:12-16 */

@@ -134,6 +134,11 @@ int run_gemm(const char *stage, int epi, void *stream, const k2w8_gemm_cfg *cfg,
 
 }  // namespace
 
+// The error channel for the library's other host sources (k2w8_checkpoint.cpp).
+int k2w8_fail_invalid(const char *message) { return fail(K2W8_INVALID_ARGUMENT, "%s", message); }
+int k2w8_fail_runtime(const char *stage, hipError_t e) { return runtime(stage, e); }
+int k2w8_succeed() { return ok(); }
+
 extern "C" {
 
 int k2w8_abi_version(void) { return K2W8_ABI_VERSION; }

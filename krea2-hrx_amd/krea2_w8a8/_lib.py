@@ -55,6 +55,28 @@ class QuantizedCfg(ctypes.Structure):
     _fields_ = [("inputs", ctypes.c_int64), ("outputs", ctypes.c_int64), ("pitch", ctypes.c_int64)]
 
 
+class TensorInfo(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32),
+        ("ndim", ctypes.c_int32),
+        ("shape", ctypes.c_int64 * 8),
+        ("data", ctypes.c_void_p),
+        ("nbytes", ctypes.c_int64),
+    ]
+
+
+class SpanInfo(ctypes.Structure):
+    _fields_ = [
+        ("device_offset", ctypes.c_int64),
+        ("device_bytes", ctypes.c_int64),
+        ("rows", ctypes.c_int64),
+        ("row_bytes", ctypes.c_int64),
+        ("device_row_bytes", ctypes.c_int64),
+        ("file_bytes", ctypes.c_int64),
+        ("segments", ctypes.c_int64),
+    ]
+
+
 class GemmCfg(ctypes.Structure):
     _fields_ = [
         ("k_size", ctypes.c_int64),
@@ -95,6 +117,18 @@ SIGNATURES = {
         ctypes.c_int,
         [_P, ctypes.POINTER(QuantizedCfg), _I64, _P, _P, _P, _P, _P, _P, _P, _P],
     ),
+    "k2w8_checkpoint_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)]),
+    "k2w8_checkpoint_close": (None, [_P]),
+    "k2w8_checkpoint_block_count": (_I64, [_P]),
+    "k2w8_checkpoint_tensor": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.POINTER(TensorInfo)]),
+    "k2w8_plan_for_checkpoint": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_void_p)]),
+    "k2w8_plan_free": (None, [_P]),
+    "k2w8_plan_total_bytes": (_I64, [_P]),
+    "k2w8_plan_layers": (_I64, [_P]),
+    "k2w8_plan_span_count": (_I64, [_P]),
+    "k2w8_plan_span_name": (ctypes.c_char_p, [_P, _I64]),
+    "k2w8_plan_span": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.POINTER(SpanInfo)]),
+    "k2w8_plan_upload": (ctypes.c_int, [_P, _P, _P, _P, _I64]),
     "k2w8_shape_gemm_pitch": (_I64, [_I64]),
     "k2w8_shape_capacity": (_I64, [_I64]),
     "k2w8_shape_gemm_grid_rows": (_I64, [_I64]),
