@@ -260,6 +260,69 @@ int k2w8_plan_span(const k2w8_plan *plan, const char *name, k2w8_span *out);
 int k2w8_plan_upload(void *stream, const k2w8_plan *plan, const k2w8_checkpoint *file,
                      void *device, int64_t device_bytes);
 
+/* ---- The W8A8 stages of a transformer block (src/session/mod.rs) ---- */
+
+/* Specialisation of a block (src/kernels/blocks.rs:38-107; production: hidden 6144,
+ * inter 16384, qkvg 15360, gate_offset 9216, eps 1e-5). */
+typedef struct k2w8_block_cfg {
+  int64_t tokens;      /* rows of x and of every activation buffer in use */
+  int64_t hidden;      /* residual width, K of qkvg/gu/wo and N of wo/down */
+  int64_t inter;       /* MLP width, K of down (gu has 2 * inter interleaved rows) */
+  int64_t qkvg;        /* columns of the fused q|k|v|gate output */
+  int64_t gate_offset; /* first column of the gate half (src/session/mod.rs:45) */
+  float eps;           /* RMSNorm epsilon */
+} k2w8_block_cfg;
+
+/* One block's resident operands (the plan's blocks.<i>.* spans). */
+typedef struct k2w8_block_weights {
+  const int8_t *qkvg_q; const float *qkvg_s;
+  const int8_t *wo_q;   const float *wo_s;
+  const int8_t *gu_q;   const float *gu_s;
+  const int8_t *down_q; const float *down_s;
+  const float *prenorm; const float *postnorm;
+} k2w8_block_weights;
+
+/* The session's workspaces (src/session/mod.rs:321-340), owned by the caller. */
+typedef struct k2w8_block_buffers {
+  void *x;           /* bf16 [tokens][hidden], the residual stream, in place */
+  int8_t *a_q;       /* int8 [tokens][pitch(max(hidden, inter))] */
+  float *a_s;        /* f32 [tokens] */
+  void *fused;       /* f16 [tokens][qkvg] */
+  void *attn_gu;     /* f16 [tokens][max(hidden, inter)]: attention output, then SwiGLU output */
+  const float *mods; /* f32 [layers][6][hidden]: prescale, preshift, pregate, postscale,
+                        postshift, postgate (src/session/mod.rs:133-138) */
+} k2w8_block_buffers;
+
+/* Session::block (src/session/mod.rs:671-711), up to the attention: prepare_norm_i8
+ * with the block's prenorm and modulation rows 0/1, then gemm_qkvg into `fused`. */
+int k2w8_block_pre_attention(void *stream, const k2w8_block_cfg *cfg, int64_t index,
+                             const k2w8_block_weights *weights, const k2w8_block_buffers *buffers);
+/* Session::block (:756-839), after the attention (whose output the caller left in
+ * attn_gu): prepare_gated_i8 over the gate half, gemm_wo + residual (gate = row 2),
+ * prepare_norm_i8 (postnorm, rows 3/4), gemm_gu + SwiGLU into attn_gu,
+ * prepare_plain_i8, gemm_down + residual (gate = row 5). */
+int k2w8_block_post_attention(void *stream, const k2w8_block_cfg *cfg, int64_t index,
+                              const k2w8_block_weights *weights, const k2w8_block_buffers *buffers);
+
+/* A recorded block loop (src/session/mod.rs:596-616): `layers` blocks, weights[i] for
+ * block i, captured once from `stream` (a created stream) into a hipGraph over the
+ * same buffers, replayed by k2w8_graph_launch. */
+typedef struct k2w8_graph k2w8_graph;
+int k2w8_blocks_record(void *stream, const k2w8_block_cfg *cfg, int64_t layers,
+                       const k2w8_block_weights *weights, const k2w8_block_buffers *buffers,
+                       k2w8_graph **out);
+int k2w8_graph_launch(void *stream, k2w8_graph *graph);
+void k2w8_graph_free(k2w8_graph *graph);
+
+/* The stage profile (src/session/mod.rs:449-479, 618-647): one eager pass over `layers`
+ * blocks with events around every launch; stage_us[k] accumulates the microseconds of
+ * stage k (labels from k2w8_block_stage_label) over all blocks. */
+int k2w8_blocks_profile(void *stream, const k2w8_block_cfg *cfg, int64_t layers,
+                        const k2w8_block_weights *weights, const k2w8_block_buffers *buffers,
+                        double *stage_us, int64_t stage_count);
+int64_t k2w8_block_stage_count(void);
+const char *k2w8_block_stage_label(int64_t index);
+
 /* Launch-shape rules of src/kernels/shape.rs:7-112. */
 int64_t k2w8_shape_gemm_pitch(int64_t k);    /* shape.rs:105-107 */
 int64_t k2w8_shape_capacity(int64_t tokens); /* shape.rs:12-16 */

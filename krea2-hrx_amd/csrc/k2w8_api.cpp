@@ -138,6 +138,14 @@ int run_gemm(const char *stage, int epi, void *stream, const k2w8_gemm_cfg *cfg,
 int k2w8_fail_invalid(const char *message) { return fail(K2W8_INVALID_ARGUMENT, "%s", message); }
 int k2w8_fail_runtime(const char *stage, hipError_t e) { return runtime(stage, e); }
 int k2w8_succeed() { return ok(); }
+// The one-time set-up of the launch paths (kernel attributes, device queries), done
+// before a stream capture so that none of it happens inside one.
+int k2w8_prime_launches() {
+  int rc = ensure_configured("blocks_record");
+  if (rc != K2W8_OK) return rc;
+  (void)k2w8::device_cus();
+  return K2W8_OK;
+}
 
 extern "C" {
 

@@ -1,0 +1,276 @@
+// The W8A8 stages of a transformer block (Session::block, src/session/mod.rs:671-840)
+// over caller-owned session buffers, the block loop recorded once into a hipGraph and
+// replayed (src/session/mod.rs:596-616), and a per-stage profile of one eager pass
+// (src/session/mod.rs:618-647, 449-479).
+//
+// Host code only: every launch goes through the library's own entry points, so the
+// argument checks and kernels are those of the single-kernel calls. The attention
+// stages between gemm_qkvg and prepare_gated (rope + q/k norm, V transpose, f16
+// attention) are outside this path: the caller runs them between
+// k2w8_block_pre_attention and k2w8_block_post_attention, leaving the attention output
+// in attn_gu.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "krea2_w8a8.h"
+
+int k2w8_fail_invalid(const char *message);
+int k2w8_fail_runtime(const char *stage, hipError_t e);
+int k2w8_succeed();
+int k2w8_prime_launches();
+
+namespace {
+
+constexpr int kModRows = 6;  // prescale, preshift, pregate, postscale, postshift, postgate
+
+int check_cfg(const k2w8_block_cfg *c, const char *stage) {
+  char msg[256];
+  if (!c) {
+    snprintf(msg, sizeof msg, "%s: null configuration", stage);
+    return k2w8_fail_invalid(msg);
+  }
+  if (c->tokens < 1 || c->hidden < 256 || c->inter < 256 || c->qkvg < c->hidden ||
+      c->gate_offset < 0 || c->gate_offset + c->hidden > c->qkvg) {
+    snprintf(msg, sizeof msg,
+             "%s: shape must have tokens >= 1, hidden and inter >= 256, and the gate half "
+             "(gate_offset + hidden) inside qkvg",
+             stage);
+    return k2w8_fail_invalid(msg);
+  }
+  return K2W8_OK;
+}
+
+const float *mod_row(const k2w8_block_buffers *b, const k2w8_block_cfg *c, int64_t index, int part) {
+  return b->mods + (index * kModRows + part) * c->hidden;
+}
+
+// One stage: a label (the reference's stage names) and the call that launches it.
+struct Stage {
+  const char *label;
+  int (*run)(void *stream, const k2w8_block_cfg *c, int64_t index, const k2w8_block_weights *w,
+             const k2w8_block_buffers *b);
+};
+
+int stage_prepare(void *s, const k2w8_block_cfg *c, int64_t i, const k2w8_block_weights *w,
+                  const k2w8_block_buffers *b) {
+  const k2w8_prepare_norm_cfg cfg = {c->hidden, k2w8_shape_gemm_pitch(c->hidden), c->eps};
+  return k2w8_prepare_norm_i8(s, &cfg, c->tokens, b->x, w->prenorm, mod_row(b, c, i, 0),
+                              mod_row(b, c, i, 1), b->a_q, b->a_s);
+}
+
+int stage_qkvg(void *s, const k2w8_block_cfg *c, int64_t, const k2w8_block_weights *w,
+               const k2w8_block_buffers *b) {
+  const int64_t pitch = k2w8_shape_gemm_pitch(c->hidden);
+  const k2w8_gemm_cfg cfg = {c->hidden, c->qkvg, pitch, k2w8_shape_gemm_m_group(), 0};
+  return k2w8_gemm_i8(s, &cfg, c->tokens, b->a_q, w->qkvg_q, w->qkvg_s, b->a_s, b->fused);
+}
+
+int stage_gated(void *s, const k2w8_block_cfg *c, int64_t, const k2w8_block_weights *,
+                const k2w8_block_buffers *b) {
+  const k2w8_prepare_gated_cfg cfg = {c->hidden, k2w8_shape_gemm_pitch(c->hidden), c->qkvg};
+  const uint16_t *gate = static_cast<const uint16_t *>(b->fused) + c->gate_offset;
+  return k2w8_prepare_gated_i8(s, &cfg, c->tokens, b->attn_gu, gate, b->a_q, b->a_s);
+}
+
+int stage_wo(void *s, const k2w8_block_cfg *c, int64_t i, const k2w8_block_weights *w,
+             const k2w8_block_buffers *b) {
+  const int64_t pitch = k2w8_shape_gemm_pitch(c->hidden);
+  const k2w8_gemm_cfg cfg = {c->hidden, c->hidden, pitch, k2w8_shape_gemm_m_group(), 0};
+  return k2w8_gemm_i8_resid(s, &cfg, c->tokens, b->a_q, w->wo_q, w->wo_s, b->a_s, b->x,
+                            mod_row(b, c, i, 2));
+}
+
+int stage_post(void *s, const k2w8_block_cfg *c, int64_t i, const k2w8_block_weights *w,
+               const k2w8_block_buffers *b) {
+  const k2w8_prepare_norm_cfg cfg = {c->hidden, k2w8_shape_gemm_pitch(c->hidden), c->eps};
+  return k2w8_prepare_norm_i8(s, &cfg, c->tokens, b->x, w->postnorm, mod_row(b, c, i, 3),
+                              mod_row(b, c, i, 4), b->a_q, b->a_s);
+}
+
+int stage_gu(void *s, const k2w8_block_cfg *c, int64_t, const k2w8_block_weights *w,
+             const k2w8_block_buffers *b) {
+  const int64_t pitch = k2w8_shape_gemm_pitch(c->hidden);
+  const k2w8_gemm_cfg cfg = {c->hidden, 2 * c->inter, pitch, k2w8_shape_gemm_m_group(), 0};
+  return k2w8_gemm_i8_swiglu(s, &cfg, c->tokens, b->a_q, w->gu_q, w->gu_s, b->a_s, b->attn_gu);
+}
+
+int stage_swiglu(void *s, const k2w8_block_cfg *c, int64_t, const k2w8_block_weights *,
+                 const k2w8_block_buffers *b) {
+  const k2w8_prepare_plain_cfg cfg = {c->inter, k2w8_shape_gemm_pitch(c->inter)};
+  return k2w8_prepare_plain_i8(s, &cfg, c->tokens, b->attn_gu, b->a_q, b->a_s);
+}
+
+int stage_down(void *s, const k2w8_block_cfg *c, int64_t i, const k2w8_block_weights *w,
+               const k2w8_block_buffers *b) {
+  const int64_t pitch = k2w8_shape_gemm_pitch(c->inter);
+  const k2w8_gemm_cfg cfg = {c->inter, c->hidden, pitch, k2w8_shape_gemm_m_group(),
+                             k2w8_shape_gemm_schedule_rows(c->tokens)};
+  return k2w8_gemm_i8_resid_256x256(s, &cfg, c->tokens, b->a_q, w->down_q, w->down_s, b->a_s,
+                                    b->x, mod_row(b, c, i, 5));
+}
+
+const Stage kPre[] = {{"prepare", stage_prepare}, {"gemm qkvg", stage_qkvg}};
+const Stage kPost[] = {{"prepare gated", stage_gated},
+                       {"gemm wo + residual", stage_wo},
+                       {"prepare", stage_post},
+                       {"gemm gate|up + swiglu", stage_gu},
+                       {"prepare swiglu", stage_swiglu},
+                       {"gemm down + residual", stage_down}};
+
+template <size_t N>
+int run_stages(const Stage (&stages)[N], void *stream, const k2w8_block_cfg *c, int64_t index,
+               const k2w8_block_weights *w, const k2w8_block_buffers *b) {
+  for (const Stage &st : stages) {
+    const int rc = st.run(stream, c, index, w, b);
+    if (rc != K2W8_OK) return rc;
+  }
+  return K2W8_OK;
+}
+
+int check_call(const k2w8_block_cfg *c, int64_t index, const k2w8_block_weights *w,
+               const k2w8_block_buffers *b, const char *stage) {
+  int rc = check_cfg(c, stage);
+  if (rc != K2W8_OK) return rc;
+  char msg[128];
+  if (!w || !b || !b->mods || index < 0) {
+    snprintf(msg, sizeof msg, "%s: null weights, buffers or modulation table", stage);
+    return k2w8_fail_invalid(msg);
+  }
+  return K2W8_OK;
+}
+
+}  // namespace
+
+struct k2w8_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  ~k2w8_graph() {
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+  }
+};
+
+extern "C" {
+
+int k2w8_block_pre_attention(void *stream, const k2w8_block_cfg *cfg, int64_t index,
+                             const k2w8_block_weights *weights, const k2w8_block_buffers *buffers) {
+  int rc = check_call(cfg, index, weights, buffers, "block_pre_attention");
+  if (rc != K2W8_OK) return rc;
+  return run_stages(kPre, stream, cfg, index, weights, buffers);
+}
+
+int k2w8_block_post_attention(void *stream, const k2w8_block_cfg *cfg, int64_t index,
+                              const k2w8_block_weights *weights, const k2w8_block_buffers *buffers) {
+  int rc = check_call(cfg, index, weights, buffers, "block_post_attention");
+  if (rc != K2W8_OK) return rc;
+  return run_stages(kPost, stream, cfg, index, weights, buffers);
+}
+
+int k2w8_blocks_record(void *stream, const k2w8_block_cfg *cfg, int64_t layers,
+                       const k2w8_block_weights *weights, const k2w8_block_buffers *buffers,
+                       k2w8_graph **out) {
+  const char *stage = "blocks_record";
+  if (!out) return k2w8_fail_invalid("blocks_record: null output");
+  *out = nullptr;
+  if (layers < 1) return k2w8_fail_invalid("blocks_record: layers must be >= 1");
+  for (int64_t i = 0; i < layers; ++i) {
+    int rc = check_call(cfg, i, weights + i, buffers, stage);
+    if (rc != K2W8_OK) return rc;
+  }
+  if (!stream)
+    return k2w8_fail_invalid("blocks_record: recording needs a created stream (not the null stream)");
+  // One-time set-up (kernel attributes, device queries) must not happen inside capture.
+  int rc = k2w8_prime_launches();
+  if (rc != K2W8_OK) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+  if (e != hipSuccess) return k2w8_fail_runtime(stage, e);
+  for (int64_t i = 0; i < layers && rc == K2W8_OK; ++i) {
+    rc = run_stages(kPre, stream, cfg, i, weights + i, buffers);
+    if (rc == K2W8_OK) rc = run_stages(kPost, stream, cfg, i, weights + i, buffers);
+  }
+  auto g = std::make_unique<k2w8_graph>();
+  e = hipStreamEndCapture(s, &g->graph);
+  if (rc != K2W8_OK) return rc;
+  if (e != hipSuccess) return k2w8_fail_runtime(stage, e);
+  e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+  if (e != hipSuccess) return k2w8_fail_runtime(stage, e);
+  *out = g.release();
+  return k2w8_succeed();
+}
+
+int k2w8_graph_launch(void *stream, k2w8_graph *graph) {
+  if (!graph || !graph->exec) return k2w8_fail_invalid("graph_launch: null graph");
+  hipError_t e = hipGraphLaunch(graph->exec, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return k2w8_fail_runtime("graph_launch", e);
+  return k2w8_succeed();
+}
+
+void k2w8_graph_free(k2w8_graph *graph) { delete graph; }
+
+int k2w8_blocks_profile(void *stream, const k2w8_block_cfg *cfg, int64_t layers,
+                        const k2w8_block_weights *weights, const k2w8_block_buffers *buffers,
+                        double *stage_us, int64_t stage_count) {
+  const char *stage = "blocks_profile";
+  const int64_t per_block = (int64_t)(sizeof kPre / sizeof kPre[0] + sizeof kPost / sizeof kPost[0]);
+  if (!stage_us || stage_count < per_block)
+    return k2w8_fail_invalid("blocks_profile: stage_us must hold k2w8_block_stage_count() values");
+  if (layers < 1) return k2w8_fail_invalid("blocks_profile: layers must be >= 1");
+  for (int64_t i = 0; i < layers; ++i) {
+    int rc = check_call(cfg, i, weights + i, buffers, stage);
+    if (rc != K2W8_OK) return rc;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  for (int64_t k = 0; k < per_block; ++k) stage_us[k] = 0.0;
+  std::vector<hipEvent_t> ev((size_t)per_block * layers + 1);
+  for (auto &x : ev) {
+    hipError_t e = hipEventCreate(&x);
+    if (e != hipSuccess) return k2w8_fail_runtime(stage, e);
+  }
+  auto destroy = [&] {
+    for (auto &x : ev) (void)hipEventDestroy(x);
+  };
+  int rc = K2W8_OK;
+  size_t at = 0;
+  hipError_t e = hipEventRecord(ev[at++], s);
+  for (int64_t i = 0; i < layers && rc == K2W8_OK && e == hipSuccess; ++i) {
+    for (const Stage &st : kPre) {
+      if ((rc = st.run(stream, cfg, i, weights + i, buffers)) != K2W8_OK) break;
+      if ((e = hipEventRecord(ev[at++], s)) != hipSuccess) break;
+    }
+    for (const Stage &st : kPost) {
+      if (rc != K2W8_OK || e != hipSuccess) break;
+      if ((rc = st.run(stream, cfg, i, weights + i, buffers)) != K2W8_OK) break;
+      if ((e = hipEventRecord(ev[at++], s)) != hipSuccess) break;
+    }
+  }
+  if (rc == K2W8_OK && e == hipSuccess) e = hipEventSynchronize(ev[at - 1]);
+  if (rc == K2W8_OK && e == hipSuccess) {
+    for (size_t k = 1; k < at; ++k) {
+      float ms = 0.0f;
+      if ((e = hipEventElapsedTime(&ms, ev[k - 1], ev[k])) != hipSuccess) break;
+      stage_us[(k - 1) % per_block] += 1e3 * (double)ms;
+    }
+  }
+  destroy();
+  if (rc != K2W8_OK) return rc;
+  if (e != hipSuccess) return k2w8_fail_runtime(stage, e);
+  return k2w8_succeed();
+}
+
+int64_t k2w8_block_stage_count(void) {
+  return (int64_t)(sizeof kPre / sizeof kPre[0] + sizeof kPost / sizeof kPost[0]);
+}
+
+const char *k2w8_block_stage_label(int64_t index) {
+  const int64_t pre = (int64_t)(sizeof kPre / sizeof kPre[0]);
+  if (index < 0 || index >= k2w8_block_stage_count()) return nullptr;
+  return index < pre ? kPre[index].label : kPost[index - pre].label;
+}
+
+}  // extern "C"

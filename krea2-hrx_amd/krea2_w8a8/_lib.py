@@ -77,6 +77,22 @@ class SpanInfo(ctypes.Structure):
     ]
 
 
+class BlockCfg(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int64) for n in ("tokens", "hidden", "inter", "qkvg", "gate_offset")] + [
+        ("eps", ctypes.c_float)
+    ]
+
+
+class BlockWeights(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "qkvg_q", "qkvg_s", "wo_q", "wo_s", "gu_q", "gu_s", "down_q", "down_s", "prenorm",
+        "postnorm")]
+
+
+class BlockBuffers(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("x", "a_q", "a_s", "fused", "attn_gu", "mods")]
+
+
 class GemmCfg(ctypes.Structure):
     _fields_ = [
         ("k_size", ctypes.c_int64),
@@ -129,6 +145,22 @@ SIGNATURES = {
     "k2w8_plan_span_name": (ctypes.c_char_p, [_P, _I64]),
     "k2w8_plan_span": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.POINTER(SpanInfo)]),
     "k2w8_plan_upload": (ctypes.c_int, [_P, _P, _P, _P, _I64]),
+    "k2w8_block_pre_attention": (
+        ctypes.c_int, [_P, ctypes.POINTER(BlockCfg), _I64, ctypes.POINTER(BlockWeights),
+                       ctypes.POINTER(BlockBuffers)]),
+    "k2w8_block_post_attention": (
+        ctypes.c_int, [_P, ctypes.POINTER(BlockCfg), _I64, ctypes.POINTER(BlockWeights),
+                       ctypes.POINTER(BlockBuffers)]),
+    "k2w8_blocks_record": (
+        ctypes.c_int, [_P, ctypes.POINTER(BlockCfg), _I64, ctypes.POINTER(BlockWeights),
+                       ctypes.POINTER(BlockBuffers), ctypes.POINTER(ctypes.c_void_p)]),
+    "k2w8_graph_launch": (ctypes.c_int, [_P, _P]),
+    "k2w8_graph_free": (None, [_P]),
+    "k2w8_blocks_profile": (
+        ctypes.c_int, [_P, ctypes.POINTER(BlockCfg), _I64, ctypes.POINTER(BlockWeights),
+                       ctypes.POINTER(BlockBuffers), ctypes.POINTER(ctypes.c_double), _I64]),
+    "k2w8_block_stage_count": (_I64, []),
+    "k2w8_block_stage_label": (ctypes.c_char_p, [_I64]),
     "k2w8_shape_gemm_pitch": (_I64, [_I64]),
     "k2w8_shape_capacity": (_I64, [_I64]),
     "k2w8_shape_gemm_grid_rows": (_I64, [_I64]),
