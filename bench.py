@@ -362,57 +362,52 @@ def skinny_sweep(k2, torch, weights, hidden, args):
 
 
 def block_linears(k2, torch, weights, hidden, args):
-    """the per-block linear sequence of a 3072-hidden DiT, M=4544, 8 blocks.
+    """the per-block linear sequence of a 3072-hidden DiT, M=4544, 8 blocks
+    with the same weights, recorded once into a hipGraph and replayed.
 
-    Per block, in the reference's order (src/session/mod.rs:671-840, attention
+    Per block, the reference's W8A8 stages in order (src/session/mod.rs:671-840, attention
     excluded): prepare_norm -> QKV [9216x3072]; prepare_gated(attn, gate) -> out-proj
     with residual [3072x3072]; prepare_norm -> SwiGLU up [2x12288x3072]; prepare_plain
-    -> down with residual [3072x12288]. Attention output and gate are synthetic.
+    -> down with residual [3072x12288]. The "attention output" is whatever the session's
+    attention buffer holds and the gate half is the QKV output's last 3072 columns.
     """
+    from krea2_w8a8.block import BlockSession
+
     M, H, I = 4544, 3072, 12288
     blocks = 8
     pitch_h, pitch_i = k2.shape.gemm_pitch(H), k2.shape.gemm_pitch(I)
-    x = hidden(M, H, 4000).to(torch.bfloat16)
-    attn = hidden(M, H, 4001).to(torch.float16)
-    gate = hidden(M, H, 4002).to(torch.float16)
-    ns = torch.rand(H, device="cuda") - 0.5
-    zero = torch.zeros(H, device="cuda")
-    one = torch.ones(H, device="cuda")
-    q = torch.empty((M, pitch_i), dtype=torch.int8, device="cuda")
-    qs = torch.empty(M, dtype=torch.float32, device="cuda")
-    qkv = torch.empty((M, 9216), dtype=torch.float16, device="cuda")
-    up = torch.empty((M, I), dtype=torch.float16, device="cuda")
     wq, sq = weights(9216, pitch_h, 4100)
     wo, so = weights(H, pitch_h, 4101)
     wgu, sgu = weights(2 * I, pitch_h, 4102)
     wd, sd = weights(H, pitch_i, 4103)
-    c_qkv = k2.GemmConfig(H, 9216, pitch_h)
-    c_o = k2.GemmConfig(H, H, pitch_h)
-    c_gu = k2.GemmConfig(H, 2 * I, pitch_h)
-    c_d = k2.GemmConfig(I, H, pitch_i, schedule_rows=int(k2.shape.gemm_schedule_rows(M)))
-
-    def block(_):
-        k2.prepare_norm_i8(x, ns, zero, zero, q, qs, width=H, out_stride=pitch_h, eps=1e-6)
-        k2.gemm_i8(q, wq, sq, qs, qkv, cfg=c_qkv)
-        k2.prepare_gated_i8(attn, gate, q, qs, width=H, out_stride=pitch_h, gate_stride=H)
-        k2.gemm_i8_resid(q, wo, so, qs, x, one, cfg=c_o)
-        k2.prepare_norm_i8(x, ns, zero, zero, q, qs, width=H, out_stride=pitch_h, eps=1e-6)
-        k2.gemm_i8_swiglu(q, wgu, sgu, qs, up, cfg=c_gu)
-        k2.prepare_plain_i8(up, q, qs, width=I, out_stride=pitch_i)
-        k2.gemm_i8_resid_256x256(q, wd, sd, qs, x, one, cfg=c_d)
-
-    def fn(i):
-        for _ in range(blocks):
-            block(i)
-
+    norm = torch.rand(H, device="cuda") - 0.5
+    block = {"qkvg_q": wq, "qkvg_s": sq, "wo_q": wo, "wo_s": so, "gu_q": wgu, "gu_s": sgu,
+             "down_q": wd, "down_s": sd, "prenorm": norm, "postnorm": norm}
+    session = BlockSession([block] * blocks, tokens=M, hidden=H, inter=I, qkvg=9216,
+                           gate_offset=6144, eps=1e-6)
+    with torch.cuda.stream(session.stream):
+        session.x.copy_(hidden(M, H, 4000).to(torch.bfloat16))
+        session.attn_gu[: M * H].copy_(hidden(M, H, 4001).to(torch.float16).reshape(-1))
+        session.mods[:, (2, 5)] = 1.0  # residual gates; scales and shifts zero
+    session.record()
     steps = max(2, args.steps // 8)
-    sec = timed(torch, fn, steps, max(1, args.warmup // 4))
+    for _ in range(max(1, args.warmup // 4)):
+        session.replay()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(session.stream):
+        e0.record()
+        for _ in range(steps):
+            session.replay()
+        e1.record()
+    session.stream.synchronize()
+    ms_block = e0.elapsed_time(e1) / (steps * blocks)
+    stages = {k: round(v / blocks, 1) for k, v in session.profile().items()}
     ops_block = 2.0 * M * H * (9216 + H + 2 * I) + 2.0 * M * I * H
-    ms_block = sec * 1e3 / blocks
-    return {"M": M, "hidden": H, "intermediate": I, "blocks": blocks,
+    return {"M": M, "hidden": H, "intermediate": I, "blocks": blocks, "replay": "hipGraph",
             "ms_per_block": round(ms_block, 4),
             "TOPS": round(ops_block / (ms_block * 1e-3) / 1e12, 1),
-            "ideal_ms_per_block_at_peak": round(ops_block / (PEAK_INT8_TOPS * 1e12) * 1e3, 4)}
+            "ideal_ms_per_block_at_peak": round(ops_block / (PEAK_INT8_TOPS * 1e12) * 1e3, 4),
+            "stage_us_per_block_eager": stages}
 
 
 def cpu_baseline(M, K, N, pitch, budget_s):
