@@ -59,7 +59,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, v16i (&acc)[FM][FN
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
         if (!live[i]) continue;
-        uint16_t *out = static_cast<uint16_t *>(g.c) + m_row[i] * (g.n >> 1) + ob;
+        uint16_t *out = static_cast<uint16_t *>(g.c) + m_row[i] * g.ldc + ob;
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
           const float gs[4] = {wg[q].x, wg[q].y, wg[q].z, wg[q].w};
@@ -105,14 +105,15 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, v16i (&acc)[FM][FN
     for (int i = 0; i < FM; ++i) {
       if (!live[i]) continue;
       if (EPI == kEpiAcc) {
-        int32_t *out = static_cast<int32_t *>(g.c) + m_row[i] * g.n + nb;
+        int32_t *out = static_cast<int32_t *>(g.c) + (int64_t)blockIdx.y * g.split_stride +
+                       m_row[i] * g.ldc + nb;
 #pragma unroll
         for (int q = 0; q < 4; ++q)
           *reinterpret_cast<v4i *>(out + 8 * q) =
               v4i{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
         continue;
       }
-      uint16_t *out = static_cast<uint16_t *>(g.c) + m_row[i] * g.n + nb;
+      uint16_t *out = static_cast<uint16_t *>(g.c) + m_row[i] * g.ldc + nb;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         uint2 prior = make_uint2(0, 0);
@@ -174,22 +175,28 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
   // m-1; their results are never stored.
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
   uint32_t a_off[kAIns], b_off[kBIns];
+  // This workgroup's K steps (all of K, or its split's share).
+  int kt_count = g.k / BK, kt_first = 0;
+  if (g.k_split_steps > 0) {
+    kt_first = (int)blockIdx.y * g.k_split_steps;
+    kt_count = min(g.k_split_steps, kt_count - kt_first);
+  }
+  const uint32_t k_first = (uint32_t)(kt_first * BK);
 #pragma unroll
   for (int i = 0; i < kAIns; ++i) {
     const int r = (wave * kAIns + i) * kRowsPerKb + lane / kCpr;
     const int c = (lane % kCpr) ^ swz_key<BK>(r);
-    a_off[i] = (uint32_t)min(m0 + r, g.m - 1) * (uint32_t)g.lda + c * 16;
+    a_off[i] = (uint32_t)min(m0 + r, g.m - 1) * (uint32_t)g.lda + c * 16 + k_first;
   }
 #pragma unroll
   for (int i = 0; i < kBIns; ++i) {
     const int r = (wave * kBIns + i) * kRowsPerKb + lane / kCpr;
     const int c = (lane % kCpr) ^ swz_key<BK>(r);
-    b_off[i] = (uint32_t)(n0 + r) * (uint32_t)g.lda + c * 16;
+    b_off[i] = (uint32_t)(n0 + r) * (uint32_t)g.lda + c * 16 + k_first;
   }
   const uint32_t a_lds = lds0 + wave * kAIns * 1024;
   const uint32_t b_lds = lds0 + BM * BK + wave * kBIns * 1024;
 
-  const int kt_count = g.k / BK;
   auto issue = [&](int kt) {
     const uint32_t so = (uint32_t)((kt % STAGES) * kStage), ko = (uint32_t)(kt * BK);
 #pragma unroll
@@ -283,7 +290,9 @@ template <int BM, int BN, int WM, int WN, int BK, int STAGES>
 hipError_t launch_tile(int epi, hipStream_t stream, const GemmArgs &a) {
   using T = TileConfig<BM, BN, WM, WN, BK, STAGES>;
   const int tiles = ((a.m + BM - 1) / BM) * (a.n / BN);
-  dim3 grid(tiles), block(T::kThreads);
+  const int k_steps = a.k / BK;
+  const int splits = a.k_split_steps > 0 ? (k_steps + a.k_split_steps - 1) / a.k_split_steps : 1;
+  dim3 grid(tiles, splits), block(T::kThreads);
   switch (epi) {
     case kEpiPlain:
       hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiPlain>), grid, block, T::kLds, stream, a);
@@ -319,7 +328,7 @@ hipError_t set_lds_tile() {
   return hipSuccess;
 }
 
-inline GemmArgs args_of(const GemmLaunch &l) {
+inline GemmArgs args_of(const GemmLaunch &l, int epilogue) {
   GemmArgs a;
   a.a = l.a;
   a.w = l.w;
@@ -333,6 +342,7 @@ inline GemmArgs args_of(const GemmLaunch &l) {
   a.k = (int)l.k;
   a.lda = (int)l.lda;
   a.m_group = l.m_group;
+  a.ldc = (int)(epilogue == kEpiSwiglu ? l.n / 2 : l.n);
   return a;
 }
 
@@ -363,7 +373,19 @@ int device_cus() {
 }
 
 // Token counts served by the few-token kernel (weights streamed, HBM-bound).
-constexpr int64_t kSkinnyMaxTokens = 128;
+#ifndef K2W8_SKINNY_MAX_TOKENS
+#define K2W8_SKINNY_MAX_TOKENS 32
+#endif
+constexpr int64_t kSkinnyMaxTokens = K2W8_SKINNY_MAX_TOKENS;
+// Fewest 128-byte K steps a split-K slice takes.
+#ifndef K2W8_SPLITK_MIN_STEPS
+#define K2W8_SPLITK_MIN_STEPS 4
+#endif
+
+size_t splitk_workspace_bytes();
+void *splitk_workspace(hipStream_t stream);
+hipError_t launch_splitk_reduce(int epilogue, hipStream_t stream, const int32_t *parts, int splits,
+                                int64_t stride, const gemm::GemmArgs &g);
 
 hipError_t configure_gemm_lds() {
   hipError_t e = gemm::set_lds_tile<256, 256, kBigWm, kBigWn, 128, 2>();
@@ -373,18 +395,86 @@ hipError_t configure_gemm_lds() {
   return e;
 }
 
-// Tile choice: the largest tile that still gives every CU a workgroup; below that,
-// the smallest tile (more workgroups than CUs matters more than per-tile efficiency).
+namespace {
+
+// Split K over 128x128 tiles when they would leave most CUs idle: enough slices to
+// give every CU a workgroup, each at least K2W8_SPLITK_MIN_STEPS K steps, within the
+// workspace. Returns the K steps per slice, or 0 for no split.
+int splitk_steps(const GemmLaunch &l, int64_t cus) {
+  const int64_t tiles = ((l.m + 127) / 128) * (l.n / 128);
+  const int64_t k_steps = l.k / 128;
+  if (tiles * 2 > cus || k_steps < 2 * K2W8_SPLITK_MIN_STEPS) return 0;
+  int64_t splits = (cus + tiles - 1) / tiles;
+  if (splits > k_steps / K2W8_SPLITK_MIN_STEPS) splits = k_steps / K2W8_SPLITK_MIN_STEPS;
+  const int64_t slice_bytes = l.m * l.n * 4;
+  const int64_t fit = (int64_t)splitk_workspace_bytes() / slice_bytes;
+  if (splits > fit) splits = fit;
+  if (splits < 2) return 0;
+  const int64_t per = (k_steps + splits - 1) / splits;
+  return (k_steps + per - 1) / per >= 2 ? (int)per : 0;
+}
+
+}  // namespace
+
+// Tile choice: the largest tile that still gives every CU a workgroup (for 256x256,
+// with a last partial round's columns re-tiled as one round of 128x128); when even
+// 64x64 tiles leave CUs idle, split K over 128x128 tiles; else the smallest tile.
 hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &l) {
   if (l.m <= kSkinnyMaxTokens) return launch_skinny(epilogue, stream, l);
-  const gemm::GemmArgs a = gemm::args_of(l);
+  gemm::GemmArgs a = gemm::args_of(l, epilogue);
   auto tiles = [&](int64_t bm, int64_t bn) { return ((l.m + bm - 1) / bm) * (l.n / bn); };
   const int64_t kCus = device_cus();
-  if (l.n % 256 == 0 && tiles(256, 256) >= kCus)
+  if (l.n % 256 == 0 && tiles(256, 256) >= kCus) {
+#ifndef K2W8_NO_TAIL_SPLIT
+    // Whole rounds of 256x256 tiles, then the columns of a last, mostly idle round as
+    // one round of 128x128 tiles (a quarter of the work each) when they fit in one.
+    const int64_t tm = (l.m + 255) / 256, total = tm * (l.n / 256);
+    const int64_t rest = total % kCus;
+    const int64_t n_big = (total / kCus) * kCus / tm * 256;
+    if (rest > 0 && rest * 2 <= kCus && n_big > 0 && n_big < l.n &&
+        ((l.m + 127) / 128) * ((l.n - n_big) / 128) <= kCus) {
+      gemm::GemmArgs big = a, tail = a;
+      big.n = (int)n_big;
+      hipError_t e = gemm::launch_tile<256, 256, kBigWm, kBigWn, 128, 2>(epilogue, stream, big);
+      if (e != hipSuccess) return e;
+      tail.n = (int)(l.n - n_big);
+      tail.w = a.w + n_big * l.lda;
+      tail.w_scale = a.w_scale + n_big;
+      if (tail.gate) tail.gate = a.gate + n_big;
+      if (tail.bias) tail.bias = a.bias + n_big;
+      const int64_t out_col = epilogue == kEpiSwiglu ? n_big / 2 : n_big;
+      const int64_t elem = epilogue == kEpiAcc ? 4 : 2;
+      tail.c = static_cast<char *>(a.c) + out_col * elem;
+      return gemm::launch_tile<128, 128, 2, 2, 128, 2>(epilogue, stream, tail);
+    }
+#endif
+    return gemm::launch_tile<256, 256, kBigWm, kBigWn, 128, 2>(epilogue, stream, a);
+  }
+  // One round of 256x256 tiles over at least half the CUs beats two rounds of 256x128.
+  if (l.n % 256 == 0 && tiles(256, 128) > kCus && 2 * tiles(256, 256) >= kCus)
     return gemm::launch_tile<256, 256, kBigWm, kBigWn, 128, 2>(epilogue, stream, a);
   if (tiles(256, 128) >= kCus)
     return gemm::launch_tile<256, 128, kMidWm, kMidWn, 128, 2>(epilogue, stream, a);
   if (tiles(128, 128) >= kCus) return gemm::launch_tile<128, 128, 2, 2, 128, 2>(epilogue, stream, a);
+  // 64x64 tiles read every operand byte 4x as often as 128x128 ones: past K=4096 the
+  // split-K pass over 128x128 tiles moves fewer bytes.
+  if (tiles(64, 64) >= kCus && l.k <= 4096)
+    return gemm::launch_tile<64, 64, 2, 2, 128, 2>(epilogue, stream, a);
+  const int per = splitk_steps(l, kCus);
+  if (per > 0) {
+    int32_t *parts = static_cast<int32_t *>(splitk_workspace(stream));
+    if (parts) {
+      const int splits = (int)((l.k / 128 + per - 1) / per);
+      gemm::GemmArgs p = a;
+      p.c = parts;
+      p.ldc = (int)l.n;
+      p.k_split_steps = per;
+      p.split_stride = l.m * l.n;
+      hipError_t e = gemm::launch_tile<128, 128, 2, 2, 128, 2>(kEpiAcc, stream, p);
+      if (e != hipSuccess) return e;
+      return launch_splitk_reduce(epilogue, stream, parts, splits, l.m * l.n, a);
+    }
+  }
   return gemm::launch_tile<64, 64, 2, 2, 128, 2>(epilogue, stream, a);
 }
 #endif

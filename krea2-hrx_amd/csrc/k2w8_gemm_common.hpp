@@ -21,6 +21,14 @@ struct GemmArgs {
   const float *gate;
   const uint16_t *bias;
   int m, n, k, lda, m_group;
+  // Row stride of c in output elements (n, or n/2 for SwiGLU, unless the launch covers
+  // a column range of a wider output).
+  int ldc = 0;
+  // Split K: workgroup row blockIdx.y runs K steps [y * k_split_steps, ...) and writes
+  // its int32 partial sums (the kEpiAcc output) at c + y * split_stride elements.
+  // 0 = no split.
+  int k_split_steps = 0;
+  int64_t split_stride = 0;
 };
 
 #ifndef K2W8_SWZ_SHIFT

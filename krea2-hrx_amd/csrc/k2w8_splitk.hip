@@ -1,0 +1,183 @@
+// Split-K for the GEMM family at shapes with too few output tiles to fill the chip
+// (the mid-M text-encoder shapes). The tile kernel runs once per K slice and writes
+// each slice's exact int32 partial sums to a workspace; this kernel adds the slices
+// (integer addition: any order gives the same sums) and applies the epilogue, with
+// the same f32 operation sequence as the tile kernels' epilogues
+// (kernels/gemm_i8_256.loom:606-626, kernels/gemm_i8_resid_256.loom:623-635,
+// kernels/gemm_i8_swiglu_256.loom:640-660).
+//
+// The workspace is one device allocation per device, made on first use outside any
+// stream capture and kept for the life of the process.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <mutex>
+
+#include "k2w8_gemm_common.hpp"
+#include "k2w8_internal.hpp"
+#include "k2w8_numerics.hpp"
+
+namespace k2w8 {
+
+namespace splitk {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+struct ReduceArgs {
+  const int32_t *parts;
+  int splits;
+  int64_t stride;  // elements between slices
+  int m, n;
+  const float *w_scale, *a_scale;
+  void *c;
+  const float *gate;
+  const uint16_t *bias;
+};
+
+__device__ __forceinline__ v4i sum_slices(const ReduceArgs &r, int64_t at) {
+  v4i acc = *reinterpret_cast<const v4i *>(r.parts + at);
+  for (int s = 1; s < r.splits; ++s) acc += *reinterpret_cast<const v4i *>(r.parts + s * r.stride + at);
+  return acc;
+}
+
+// One work item: four consecutive channels of one row (SwiGLU: four gate channels and
+// their four up channels, 16 rows further on in the 32-row group).
+template <int EPI>
+__global__ __launch_bounds__(256) void reduce_kernel(ReduceArgs r) {
+  const int64_t per_row = EPI == kEpiSwiglu ? r.n / 8 : r.n / 4;
+  const int64_t total = (int64_t)r.m * per_row;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int m = (int)(t / per_row);
+    const int g = (int)(t - (int64_t)m * per_row);
+    if (EPI == kEpiSwiglu) {
+      const int nb = (g >> 2) * 32 + (g & 3) * 4;  // gate channels nb..nb+3
+      const int64_t row = (int64_t)m * r.n;
+      const v4i ag = sum_slices(r, row + nb), au = sum_slices(r, row + nb + 16);
+      const float as = r.a_scale[m];
+      const float4 gs = *reinterpret_cast<const float4 *>(r.w_scale + nb);
+      const float4 us = *reinterpret_cast<const float4 *>(r.w_scale + nb + 16);
+      const float gsv[4] = {gs.x, gs.y, gs.z, gs.w}, usv[4] = {us.x, us.y, us.z, us.w};
+      uint32_t packed[2];
+#pragma unroll
+      for (int e = 0; e < 4; e += 2) {
+        float g0 = ((float)ag[e] * gsv[e]) * as, g1 = ((float)ag[e + 1] * gsv[e + 1]) * as;
+        float u0 = ((float)au[e] * usv[e]) * as, u1 = ((float)au[e + 1] * usv[e + 1]) * as;
+        bf16_round2(g0, g1);
+        bf16_round2(u0, u1);
+        float s0 = g0 * sigmoid(g0), s1 = g1 * sigmoid(g1);
+        bf16_round2(s0, s1);
+        float p0 = s0 * u0, p1 = s1 * u1;
+        bf16_round2(p0, p1);
+        packed[e >> 1] = f16_pack2(p0, p1);
+      }
+      const int o = (g >> 2) * 16 + (g & 3) * 4;
+      *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(r.c) + (int64_t)m * (r.n >> 1) + o) =
+          make_uint2(packed[0], packed[1]);
+      continue;
+    }
+    const int nb = g * 4;
+    const int64_t at = (int64_t)m * r.n + nb;
+    const v4i acc = sum_slices(r, at);
+    if (EPI == kEpiAcc) {
+      *reinterpret_cast<v4i *>(static_cast<int32_t *>(r.c) + at) = acc;
+      continue;
+    }
+    const float as = r.a_scale[m];
+    const float4 w4 = *reinterpret_cast<const float4 *>(r.w_scale + nb);
+    const float ws[4] = {w4.x, w4.y, w4.z, w4.w};
+    float extra[4] = {0.f, 0.f, 0.f, 0.f};
+    if (EPI == kEpiResid) {
+      const float4 v = *reinterpret_cast<const float4 *>(r.gate + nb);
+      extra[0] = v.x; extra[1] = v.y; extra[2] = v.z; extra[3] = v.w;
+    }
+    if (EPI == kEpiBias) {
+      const uint2 v = *reinterpret_cast<const uint2 *>(r.bias + nb);
+      extra[0] = f16_value(v.x & 0xffffu); extra[1] = f16_value(v.x >> 16);
+      extra[2] = f16_value(v.y & 0xffffu); extra[3] = f16_value(v.y >> 16);
+    }
+    uint16_t *out = static_cast<uint16_t *>(r.c) + at;
+    uint32_t prior[2] = {0u, 0u};
+    if (EPI == kEpiResid) {
+      const uint2 p = *reinterpret_cast<const uint2 *>(out);
+      prior[0] = p.x;
+      prior[1] = p.y;
+    }
+    uint32_t packed[2];
+#pragma unroll
+    for (int e = 0; e < 4; e += 2) {
+      float v0 = ((float)acc[e] * ws[e]) * as, v1 = ((float)acc[e + 1] * ws[e + 1]) * as;
+      if (EPI == kEpiBias) {
+        v0 = v0 + extra[e];
+        v1 = v1 + extra[e + 1];
+      }
+      bf16_round2(v0, v1);
+      if (EPI == kEpiResid) {  // x = bf16(x + bf16(gate * bf16(v)))
+        float g0 = v0 * extra[e], g1 = v1 * extra[e + 1];
+        bf16_round2(g0, g1);
+        const uint32_t w = prior[e >> 1];
+        packed[e >> 1] = bf16_pack2(__uint_as_float(w << 16) + g0, __uint_as_float(w & 0xffff0000u) + g1);
+      } else {
+        packed[e >> 1] = f16_pack2(v0, v1);
+      }
+    }
+    *reinterpret_cast<uint2 *>(out) = make_uint2(packed[0], packed[1]);
+  }
+}
+
+constexpr size_t kWorkspaceBytes = size_t(64) << 20;
+constexpr int kMaxDevices = 64;
+std::mutex g_lock;
+void *g_workspace[kMaxDevices];
+
+}  // namespace splitk
+
+size_t splitk_workspace_bytes() { return splitk::kWorkspaceBytes; }
+
+void *splitk_workspace(hipStream_t stream) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= splitk::kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> guard(splitk::g_lock);
+  if (splitk::g_workspace[dev]) return splitk::g_workspace[dev];
+  // Never allocate inside a stream capture: the caller then runs without split-K.
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  if (stream && hipStreamIsCapturing(stream, &status) != hipSuccess) return nullptr;
+  if (status != hipStreamCaptureStatusNone) return nullptr;
+  void *p = nullptr;
+  if (hipMalloc(&p, splitk::kWorkspaceBytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  splitk::g_workspace[dev] = p;
+  return p;
+}
+
+hipError_t launch_splitk_reduce(int epilogue, hipStream_t stream, const int32_t *parts, int splits,
+                                int64_t stride, const gemm::GemmArgs &g) {
+  splitk::ReduceArgs r;
+  r.parts = parts;
+  r.splits = splits;
+  r.stride = stride;
+  r.m = g.m;
+  r.n = g.n;
+  r.w_scale = g.w_scale;
+  r.a_scale = g.a_scale;
+  r.c = g.c;
+  r.gate = g.gate;
+  r.bias = g.bias;
+  const int64_t items = (int64_t)g.m * (epilogue == kEpiSwiglu ? g.n / 8 : g.n / 4);
+  int64_t blocks = (items + 255) / 256;
+  const int64_t cap = (int64_t)device_cus() * 8;
+  if (blocks > cap) blocks = cap;
+  dim3 grid((unsigned)(blocks > 0 ? blocks : 1)), block(256);
+  switch (epilogue) {
+    case kEpiPlain: hipLaunchKernelGGL(splitk::reduce_kernel<kEpiPlain>, grid, block, 0, stream, r); break;
+    case kEpiResid: hipLaunchKernelGGL(splitk::reduce_kernel<kEpiResid>, grid, block, 0, stream, r); break;
+    case kEpiSwiglu: hipLaunchKernelGGL(splitk::reduce_kernel<kEpiSwiglu>, grid, block, 0, stream, r); break;
+    case kEpiBias: hipLaunchKernelGGL(splitk::reduce_kernel<kEpiBias>, grid, block, 0, stream, r); break;
+    default: hipLaunchKernelGGL(splitk::reduce_kernel<kEpiAcc>, grid, block, 0, stream, r); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace k2w8

@@ -91,6 +91,16 @@ SHAPES = [
     (1000, 3072, 768, 0),
     (513, 2560, 4096, 0),
     (2000, 256, 8192, 64),  # >= 256 tiles of 256x256: the wide-tile kernel
+    # whole rounds of 256x256 tiles, then the last columns as one round of 128x128
+    (2000, 256, 9216, 64),
+    # one round of 256x256 tiles where 256x128 would take two
+    (300, 256, 19456, 0),
+    # split K over 128x128 tiles (fewer than half the CUs get a tile; or 64x64 tiles
+    # would fill the chip but K is long)
+    (320, 4224, 4096, 0),
+    (256, 9728, 2560, 0),
+    (129, 2560, 4096, 64),
+    (300, 1024, 512, 0),
     # few-token kernel: K ranges that leave single 64-byte steps per wave, 1..4 blocks
     (2, 384, 256, 0),
     (16, 2560, 512, 0),
