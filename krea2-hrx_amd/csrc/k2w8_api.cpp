@@ -144,6 +144,9 @@ int k2w8_prime_launches() {
   int rc = ensure_configured("blocks_record");
   if (rc != K2W8_OK) return rc;
   (void)k2w8::device_cus();
+  // Allocate the split-K workspace now, outside the capture, so recorded GEMMs may
+  // split K as eager ones do.
+  (void)k2w8::splitk_workspace(nullptr);
   return K2W8_OK;
 }
 

@@ -382,8 +382,6 @@ constexpr int64_t kSkinnyMaxTokens = K2W8_SKINNY_MAX_TOKENS;
 #define K2W8_SPLITK_MIN_STEPS 4
 #endif
 
-size_t splitk_workspace_bytes();
-void *splitk_workspace(hipStream_t stream);
 hipError_t launch_splitk_reduce(int epilogue, hipStream_t stream, const int32_t *parts, int splits,
                                 int64_t stride, const gemm::GemmArgs &g);
 

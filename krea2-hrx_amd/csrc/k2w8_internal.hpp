@@ -44,4 +44,10 @@ hipError_t launch_transport(int direction, hipStream_t stream, int64_t count, co
 // Multiprocessor (CU) count of the current device, cached per device ordinal.
 int device_cus();
 
+// The split-K GEMMs' int32 partial-sum workspace of the current device: allocated on
+// first use (never while `stream` is capturing; nullptr then, and the GEMM runs
+// without split-K), kept until the process ends.
+size_t splitk_workspace_bytes();
+void *splitk_workspace(hipStream_t stream);
+
 }  // namespace k2w8
