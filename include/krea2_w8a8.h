@@ -191,6 +191,88 @@ int k2w8_quantized_forward(void *stream, const k2w8_quantized_cfg *cfg, int64_t 
                            void *transport, int8_t *quantized, float *q_scales, void *out_f16,
                            void *out);
 
+/* ---- The attention step of a block (src/session/mod.rs:714-755) ---- */
+
+/* kernels/rope_qknorm_f16.loom:12-20 */
+typedef struct k2w8_rope_qknorm_cfg {
+  int64_t row_stride; /* qkv row pitch in elements; multiple of 128, 128..65536 */
+  int64_t q_heads;    /* 1..256 */
+  int64_t kv_heads;   /* 1..256 */
+  int64_t k_offset;   /* first k column; multiple of 128, 128..65536 */
+  float eps;
+} k2w8_rope_qknorm_cfg;
+
+/*
+ * rope_qknorm_f16: replaces krea2_rope_qknorm_f16 (kernels/rope_qknorm_f16.loom:22-159).
+ * Bindings in the reference's order (:24):
+ *   qkv f16 [tokens][row_stride]: q heads at column 0, k heads at k_offset, v heads at
+ *       k_offset + kv_heads*128 (the fused qkvg GEMM output)
+ *   q_scale, k_scale f32 [128]: zero-centred RMSNorm scales (multiplier 1 + scale)
+ *   cos, sin f32 [tokens][128]
+ *   q_out f16 [tokens][q_heads*128], k_out, v_out f16 [tokens][kv_heads*128]
+ * Per head: x = bf16(h / sqrt(mean(h^2) + eps) * (1 + scale[c])), then the rotary
+ * pairs (2i, 2i+1) -> bf16(x0 cos - x1 sin), bf16(x1 cos + x0 sin), stored as f16;
+ * v heads are copied. tokens in 1..2^20; every buffer 16-byte aligned.
+ */
+int k2w8_rope_qknorm_f16(void *stream, const k2w8_rope_qknorm_cfg *cfg, int64_t tokens,
+                         const void *qkv, const float *q_scale, const float *k_scale,
+                         const float *cos, const float *sin, void *q_out, void *k_out,
+                         void *v_out);
+
+/* kernels/native/v_transpose.loom:7-9 */
+typedef struct k2w8_v_transpose_cfg {
+  int64_t width;        /* multiple of 32, 32..65536 */
+  int64_t row_capacity; /* multiple of 32, 32..2^20 */
+} k2w8_v_transpose_cfg;
+
+/*
+ * v_transpose: replaces krea2_v_transpose (kernels/native/v_transpose.loom:11-90,
+ * src/session/v_transpose.rs): x f16 [rows][width] -> out f16 [width][row_capacity].
+ * Columns at or past `rows` are not written: the caller keeps them zero (the attention
+ * kernel reads them). rows in 1..row_capacity; x and out 16-byte aligned.
+ */
+int k2w8_v_transpose(void *stream, const k2w8_v_transpose_cfg *cfg, int64_t rows, const void *x,
+                     void *out);
+
+/* kernels/attention_gqa_lds_f16_wmma.loom:18-28 */
+typedef struct k2w8_attention_cfg {
+  int64_t q_stride;       /* q row pitch in elements; multiple of 128, 128..32768 */
+  int64_t kv_stride;      /* k row pitch and V^T rows; multiple of 128, 128..32768 */
+  int64_t out_stride;     /* out row pitch; multiple of 128, 128..32768 */
+  int64_t tokens;         /* keys and queries: 16..65536 */
+  int64_t token_capacity; /* rows of q and k, columns of V^T: multiple of 16, >= tokens + 16 */
+  float scale;            /* score scale, 1/sqrt(128) in production */
+} k2w8_attention_cfg;
+
+/*
+ * attention_f16: replaces krea2_attention_gqa_lds_f16_wmma and its 32-query twin
+ * (kernels/attention_gqa_lds_f16_wmma.loom:30-380, _q32.loom), non-causal grouped-query
+ * attention with four query heads per key-value head (query head h reads kv head h/4).
+ * Bindings in the reference's order (:35):
+ *   q f16 [token_capacity][q_stride], k f16 [token_capacity][kv_stride],
+ *   v = V^T f16 [kv_stride][token_capacity] (as k2w8_v_transpose writes it),
+ *   out f16 [token_count][out_stride]
+ * out[t][h*128 + c] = sum_j softmax_j(scale * q_t.k_j) v_j[c] over keys j < tokens, with
+ * fp16 products, f32 accumulation and an f32 online softmax whose weights are rounded
+ * to f16 for the PV product. Rows t < min(tokens, token_count) are written. Rows of q
+ * and k and columns of V^T past `tokens` must be zero. kv_head_count in 1..
+ * kv_stride/128, with 4 * kv_head_count * 128 <= q_stride and <= out_stride.
+ */
+int k2w8_attention_f16(void *stream, const k2w8_attention_cfg *cfg, int64_t token_count,
+                       int64_t kv_head_count, const void *q, const void *k, const void *v,
+                       void *out);
+
+/*
+ * attention_f16_grouped: k2w8_attention_f16 with `group` query heads per key-value head
+ * (1, 2 or 4; query head h reads kv head h / group). An extension: the reference kernel
+ * fixes the group at 4; the block entry points use this for head layouts whose ratio
+ * differs. Same bindings and rules, with group * kv_head_count * 128 in place of
+ * 4 * kv_head_count * 128.
+ */
+int k2w8_attention_f16_grouped(void *stream, const k2w8_attention_cfg *cfg, int64_t token_count,
+                               int64_t kv_head_count, int64_t group, const void *q, const void *k,
+                               const void *v, void *out);
+
 /* ---- Checkpoint upload (host code; src/checkpoint/, src/session/weights.rs) ---- */
 
 /* Tensor element types of a .safetensors header. */

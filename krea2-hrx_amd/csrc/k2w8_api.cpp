@@ -287,6 +287,134 @@ int k2w8_lora_transport(void *stream, int direction, int64_t count, const void *
   return ok();
 }
 
+// kernels/rope_qknorm_f16.loom:12-20, 22-159
+int k2w8_rope_qknorm_f16(void *stream, const k2w8_rope_qknorm_cfg *cfg, int64_t tokens,
+                         const void *qkv, const float *q_scale, const float *k_scale,
+                         const float *cos, const float *sin, void *q_out, void *k_out,
+                         void *v_out) {
+  const char *stage = "rope_qknorm_f16";
+  if (!cfg) return fail(K2W8_INVALID_ARGUMENT, "%s: null configuration", stage);
+  if (cfg->row_stride < 128 || cfg->row_stride > 65536 || cfg->row_stride % 128)
+    return fail(K2W8_INVALID_ARGUMENT, "%s: row_stride must be a multiple of 128 in 128..65536, got %lld",
+                stage, (long long)cfg->row_stride);
+  if (cfg->q_heads < 1 || cfg->q_heads > 256 || cfg->kv_heads < 1 || cfg->kv_heads > 256)
+    return fail(K2W8_INVALID_ARGUMENT, "%s: q_heads and kv_heads must be in 1..256", stage);
+  if (cfg->k_offset < 128 || cfg->k_offset > 65536 || cfg->k_offset % 128)
+    return fail(K2W8_INVALID_ARGUMENT, "%s: k_offset must be a multiple of 128 in 128..65536, got %lld",
+                stage, (long long)cfg->k_offset);
+  if (cfg->q_heads * 128 > cfg->row_stride || cfg->k_offset + 2 * cfg->kv_heads * 128 > cfg->row_stride)
+    return fail(K2W8_INVALID_ARGUMENT, "%s: q heads and k_offset + 2 * kv_heads * 128 must fit row_stride",
+                stage);
+  if (!(cfg->eps >= 0.0f)) return fail(K2W8_INVALID_ARGUMENT, "%s: eps must be >= 0", stage);
+  if (tokens < 1 || tokens > (int64_t(1) << 20))
+    return fail(K2W8_INVALID_ARGUMENT, "%s: tokens must be in 1..2^20, got %lld", stage, (long long)tokens);
+  if (!qkv || !q_scale || !k_scale || !cos || !sin || !q_out || !k_out || !v_out)
+    return fail(K2W8_INVALID_ARGUMENT, "%s: null buffer", stage);
+  for (const void *p : {qkv, (const void *)q_scale, (const void *)k_scale, (const void *)cos,
+                        (const void *)sin, (const void *)q_out, (const void *)k_out, (const void *)v_out})
+    if (!aligned(p, 16)) return fail(K2W8_INVALID_ARGUMENT, "%s: every buffer must be 16-byte aligned", stage);
+  k2w8::RopeLaunch l;
+  l.qkv = qkv;
+  l.q_scale = q_scale;
+  l.k_scale = k_scale;
+  l.cos = cos;
+  l.sin = sin;
+  l.q_out = q_out;
+  l.k_out = k_out;
+  l.v_out = v_out;
+  l.tokens = tokens;
+  l.row_stride = cfg->row_stride;
+  l.q_heads = cfg->q_heads;
+  l.kv_heads = cfg->kv_heads;
+  l.k_offset = cfg->k_offset;
+  l.eps = cfg->eps;
+  hipError_t e = k2w8::launch_rope_qknorm(static_cast<hipStream_t>(stream), l);
+  if (e != hipSuccess) return runtime(stage, e);
+  return ok();
+}
+
+// kernels/native/v_transpose.loom:7-9, 11-90
+int k2w8_v_transpose(void *stream, const k2w8_v_transpose_cfg *cfg, int64_t rows, const void *x,
+                     void *out) {
+  const char *stage = "v_transpose";
+  if (!cfg) return fail(K2W8_INVALID_ARGUMENT, "%s: null configuration", stage);
+  if (cfg->width < 32 || cfg->width > 65536 || cfg->width % 32)
+    return fail(K2W8_INVALID_ARGUMENT, "%s: width must be a multiple of 32 in 32..65536, got %lld", stage,
+                (long long)cfg->width);
+  if (cfg->row_capacity < 32 || cfg->row_capacity > (int64_t(1) << 20) || cfg->row_capacity % 32)
+    return fail(K2W8_INVALID_ARGUMENT, "%s: row_capacity must be a multiple of 32 in 32..2^20, got %lld",
+                stage, (long long)cfg->row_capacity);
+  if (rows < 1 || rows > cfg->row_capacity)
+    return fail(K2W8_INVALID_ARGUMENT, "%s: rows must be in 1..row_capacity, got %lld", stage,
+                (long long)rows);
+  if (!x || !out) return fail(K2W8_INVALID_ARGUMENT, "%s: null buffer", stage);
+  if (!aligned(x, 16) || !aligned(out, 16))
+    return fail(K2W8_INVALID_ARGUMENT, "%s: x and out must be 16-byte aligned", stage);
+  hipError_t e = k2w8::launch_v_transpose(static_cast<hipStream_t>(stream), rows, cfg->width,
+                                          cfg->row_capacity, x, out);
+  if (e != hipSuccess) return runtime(stage, e);
+  return ok();
+}
+
+// kernels/attention_gqa_lds_f16_wmma.loom:18-28, 30-380
+int k2w8_attention_f16(void *stream, const k2w8_attention_cfg *cfg, int64_t token_count,
+                       int64_t kv_head_count, const void *q, const void *k, const void *v,
+                       void *out) {
+  return k2w8_attention_f16_grouped(stream, cfg, token_count, kv_head_count, 4, q, k, v, out);
+}
+
+int k2w8_attention_f16_grouped(void *stream, const k2w8_attention_cfg *cfg, int64_t token_count,
+                               int64_t kv_head_count, int64_t group, const void *q, const void *k,
+                               const void *v, void *out) {
+  const char *stage = "attention_f16";
+  if (group != 1 && group != 2 && group != 4)
+    return fail(K2W8_INVALID_ARGUMENT, "%s: group must be 1, 2 or 4, got %lld", stage, (long long)group);
+  if (!cfg) return fail(K2W8_INVALID_ARGUMENT, "%s: null configuration", stage);
+  for (int64_t s : {cfg->q_stride, cfg->kv_stride, cfg->out_stride})
+    if (s < 128 || s > 32768 || s % 128)
+      return fail(K2W8_INVALID_ARGUMENT, "%s: strides must be multiples of 128 in 128..32768, got %lld",
+                  stage, (long long)s);
+  if (cfg->tokens < 16 || cfg->tokens > 65536)
+    return fail(K2W8_INVALID_ARGUMENT, "%s: tokens must be in 16..65536, got %lld", stage,
+                (long long)cfg->tokens);
+  if (cfg->token_capacity % 16 || cfg->token_capacity > (int64_t(1) << 20) ||
+      cfg->token_capacity < cfg->tokens + 16)
+    return fail(K2W8_INVALID_ARGUMENT,
+                "%s: token_capacity must be a multiple of 16, >= tokens + 16 and <= 2^20, got %lld", stage,
+                (long long)cfg->token_capacity);
+  if (!(cfg->scale > 0.0f) || !(cfg->scale < 1e30f))
+    return fail(K2W8_INVALID_ARGUMENT, "%s: scale must be positive and finite", stage);
+  if (token_count < 1 || token_count > cfg->token_capacity)
+    return fail(K2W8_INVALID_ARGUMENT, "%s: token_count must be in 1..token_capacity, got %lld", stage,
+                (long long)token_count);
+  if (kv_head_count < 1 || kv_head_count * 128 > cfg->kv_stride ||
+      group * kv_head_count * 128 > cfg->q_stride || group * kv_head_count * 128 > cfg->out_stride)
+    return fail(K2W8_INVALID_ARGUMENT,
+                "%s: kv_head_count must be >= 1 with kv_head_count*128 <= kv_stride and "
+                "group*kv_head_count*128 <= q_stride, out_stride (got %lld)",
+                stage, (long long)kv_head_count);
+  if (!q || !k || !v || !out) return fail(K2W8_INVALID_ARGUMENT, "%s: null buffer", stage);
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(out, 16))
+    return fail(K2W8_INVALID_ARGUMENT, "%s: q, k, v and out must be 16-byte aligned", stage);
+  k2w8::AttentionLaunch l;
+  l.q = q;
+  l.k = k;
+  l.vt = v;
+  l.out = out;
+  l.tokens = cfg->tokens;
+  l.rows_out = token_count < cfg->tokens ? token_count : cfg->tokens;
+  l.capacity = cfg->token_capacity;
+  l.q_stride = cfg->q_stride;
+  l.kv_stride = cfg->kv_stride;
+  l.out_stride = cfg->out_stride;
+  l.kv_heads = kv_head_count;
+  l.group = group;
+  l.scale = cfg->scale;
+  hipError_t e = k2w8::launch_attention(static_cast<hipStream_t>(stream), l);
+  if (e != hipSuccess) return runtime(stage, e);
+  return ok();
+}
+
 // src/training/quantized.rs:51-112
 int k2w8_quantized_forward(void *stream, const k2w8_quantized_cfg *cfg, int64_t rows,
                            const void *x, const int8_t *weight, const float *scales,

@@ -1,0 +1,389 @@
+// The attention step of a block, between the fused qkvg GEMM and the gated prepare
+// (src/session/mod.rs:714-755): per-head RMSNorm + rotary embedding on q and k, the
+// V transpose, and fp16 grouped-query attention with an f32 online softmax.
+//
+//   rope_qknorm  kernels/rope_qknorm_f16.loom:1-159
+//   v_transpose  kernels/native/v_transpose.loom (V [tokens][width] -> [width][capacity])
+//   attention    kernels/attention_gqa_lds_f16_wmma.loom:1-380 (and its 32-query twin)
+//
+// rope_qknorm and v_transpose are HBM-bound elementwise passes. The attention kernel
+// is MFMA-bound: a workgroup of four waves owns one key-value head and its `group`
+// query heads (4 in the reference's layout: one wave per query head, 32 query tokens;
+// 2: two waves per head, 64 tokens; 1: 128 tokens). Each 64-key tile of K and V^T is staged once
+// in LDS and serves all four waves. A wave computes S^T = K Q^T with
+// v_mfma_f32_32x32x16_f16 (keys as rows), so each lane holds one query's scores and
+// the softmax needs only one cross-lane exchange (lanes l and l^32); the f16
+// probabilities then feed O^T = V^T P^T straight from the accumulator registers, and
+// the per-query rescale is a per-lane scalar.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "k2w8_internal.hpp"
+#include "k2w8_numerics.hpp"
+
+namespace k2w8 {
+
+namespace attn {
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+constexpr int kXcds = 8;
+
+// ---------------------------------------------------------------------------------
+// rope_qknorm: one 16-lane group per (token, head); lane j holds channels 8j..8j+7 of
+// the head. Heads [0, q_heads) are q, then kv_heads of k, then kv_heads of v (copied).
+//   ss   = sum of squares: lane partial ((x0^2+x1^2)+(x2^2+x3^2))+((x4^2+x5^2)+(x6^2+x7^2)),
+//          then an xor butterfly over offsets 1, 2, 4, 8 (every lane ends with the same sum)
+//   r    = 1 / sqrt(ss * (1/128) + eps)                     (correctly rounded)
+//   x    = bf16((h * r) * (scale[c] + 1))
+//   out  = f16(bf16(x[c] * cos[c] -/+ x[partner] * sin[c]))  (pairs 2i, 2i+1)
+// ---------------------------------------------------------------------------------
+struct RopeArgs {
+  const uint16_t *qkv;
+  const float *q_scale, *k_scale, *cos, *sin;
+  uint16_t *q_out, *k_out, *v_out;
+  uint32_t items;  // tokens * heads
+  int heads, row_stride, q_heads, kv_heads, k_offset;
+  float eps;
+};
+
+__device__ __forceinline__ float unpack_lo(uint32_t w) { return f16_value((uint16_t)(w & 0xffffu)); }
+__device__ __forceinline__ float unpack_hi(uint32_t w) { return f16_value((uint16_t)(w >> 16)); }
+
+__global__ __launch_bounds__(256) void rope_qknorm_kernel(RopeArgs r) {
+  const uint32_t item = blockIdx.x * 16u + (threadIdx.x >> 4);
+  const int j = threadIdx.x & 15;
+  if (item >= r.items) return;  // the 16 lanes of an item leave together
+  const uint32_t t = item / (uint32_t)r.heads;
+  const int head = (int)(item - t * (uint32_t)r.heads);
+  const bool is_q = head < r.q_heads;
+  const bool is_v = head >= r.q_heads + r.kv_heads;
+  const int kh = is_q ? 0 : head - r.q_heads;
+  const int vh = is_v ? head - r.q_heads - r.kv_heads : 0;
+  const int col = is_q ? head * 128 : (is_v ? r.k_offset + r.kv_heads * 128 + vh * 128 : r.k_offset + kh * 128);
+  const v4u in = *reinterpret_cast<const v4u *>(r.qkv + (int64_t)t * r.row_stride + col + 8 * j);
+  const int64_t kv_row = (int64_t)t * r.kv_heads * 128;
+  if (is_v) {
+    *reinterpret_cast<v4u *>(r.v_out + kv_row + vh * 128 + 8 * j) = in;
+    return;
+  }
+  float x[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = unpack_lo(in[i]);
+    x[2 * i + 1] = unpack_hi(in[i]);
+  }
+  float ss = ((x[0] * x[0] + x[1] * x[1]) + (x[2] * x[2] + x[3] * x[3])) +
+             ((x[4] * x[4] + x[5] * x[5]) + (x[6] * x[6] + x[7] * x[7]));
+  ss += __shfl_xor(ss, 1, 16);
+  ss += __shfl_xor(ss, 2, 16);
+  ss += __shfl_xor(ss, 4, 16);
+  ss += __shfl_xor(ss, 8, 16);
+  const float rinv = 1.0f / __builtin_sqrtf(ss * 0.0078125f + r.eps);
+  const float *scale = (is_q ? r.q_scale : r.k_scale) + 8 * j;
+  const float4 s0 = *reinterpret_cast<const float4 *>(scale);
+  const float4 s1 = *reinterpret_cast<const float4 *>(scale + 4);
+  const float sc[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+  const float *cs = r.cos + (int64_t)t * 128 + 8 * j;
+  const float *sn = r.sin + (int64_t)t * 128 + 8 * j;
+  const float4 c0 = *reinterpret_cast<const float4 *>(cs), c1 = *reinterpret_cast<const float4 *>(cs + 4);
+  const float4 n0 = *reinterpret_cast<const float4 *>(sn), n1 = *reinterpret_cast<const float4 *>(sn + 4);
+  const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  const float sv[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
+  v4u o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float a = (x[2 * i] * rinv) * (sc[2 * i] + 1.0f);
+    float b = (x[2 * i + 1] * rinv) * (sc[2 * i + 1] + 1.0f);
+    bf16_round2(a, b);
+    float ra = a * cv[2 * i] - b * sv[2 * i];
+    float rb = b * cv[2 * i + 1] + a * sv[2 * i + 1];
+    bf16_round2(ra, rb);
+    o[i] = f16_pack2(ra, rb);
+  }
+  uint16_t *dst = is_q ? r.q_out + (int64_t)t * r.q_heads * 128 + head * 128 : r.k_out + kv_row + kh * 128;
+  *reinterpret_cast<v4u *>(dst + 8 * j) = o;
+}
+
+// ---------------------------------------------------------------------------------
+// v_transpose: [rows][width] f16 -> [width][capacity] f16 through a 64x64 LDS tile.
+// Output columns at or past `rows` are never written (the caller's zero headroom).
+// ---------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void v_transpose_kernel(const uint16_t *x, uint16_t *out, int rows,
+                                                          int width, int capacity) {
+  __shared__ __attribute__((aligned(16))) uint16_t tile[64][72];
+  const int r0 = blockIdx.x * 64, c0 = blockIdx.y * 64;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int row = (tid >> 3) + 32 * p, ch = (tid & 7) * 8;
+    v4u v = {0u, 0u, 0u, 0u};
+    if (r0 + row < rows && c0 + ch < width)
+      v = *reinterpret_cast<const v4u *>(x + (int64_t)(r0 + row) * width + c0 + ch);
+    *reinterpret_cast<v4u *>(&tile[row][ch]) = v;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int ch = (tid >> 3) + 32 * p, tk = (tid & 7) * 8;
+    if (c0 + ch >= width) continue;
+    uint16_t e[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) e[i] = tile[tk + i][ch];
+    uint16_t *dst = out + (int64_t)(c0 + ch) * capacity + r0 + tk;
+    if (r0 + tk + 8 <= rows) {
+      v4u v;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = (uint32_t)e[2 * i] | ((uint32_t)e[2 * i + 1] << 16);
+      *reinterpret_cast<v4u *>(dst) = v;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (r0 + tk + i < rows) dst[i] = e[i];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// attention: grid of (query blocks of 128/group tokens) x kv_heads workgroups,
+// renumbered XCD-major so that the workgroups of one key-value head share an XCD's L2.
+// 256 threads: wave w computes query head kv_head*group + w % group for the 32 query
+// tokens starting at the block's first + 32 * (w / group).
+//
+// LDS, two stages of 32 KiB:
+//   K tile   [64 keys][128 ch] f16, 256-byte rows, 16-byte chunk c of row r at c ^ (r & 15)
+//   V^T tile [128 ch][64 keys] f16, 128-byte rows, chunk c of row r at c ^ ((r >> 1) & 7);
+//            within each 16-key group, chunk 2g holds keys {0-3, 8-11} and chunk 2g+1
+//            keys {4-7, 12-15}: the key order of a lane half's probability registers.
+// ---------------------------------------------------------------------------------
+struct AttnArgs {
+  const uint16_t *q, *k, *vt;
+  uint16_t *out;
+  int tokens, rows_out, capacity, q_stride, kv_stride, out_stride, kv_heads, q_blocks, group;
+  float scale_log2;  // scale * log2(e): softmax in base 2
+};
+
+constexpr int kKeys = 64;
+constexpr int kStage = 2 * 16384;
+
+__device__ __forceinline__ int k_addr(int row, int chunk) { return row * 256 + ((chunk ^ (row & 15)) << 4); }
+__device__ __forceinline__ int v_addr(int row, int chunk) {
+  return 16384 + row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4);
+}
+
+struct TileRegs {
+  v4u k[4], v[4];
+};
+
+__device__ __forceinline__ void load_tile(const AttnArgs &a, int kv_head, int key0, int tid, TileRegs &t) {
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int idx = tid + 256 * p;
+    const int row = idx >> 4, chunk = idx & 15;
+    const int key = min(key0 + row, a.capacity - 1);
+    t.k[p] = *reinterpret_cast<const v4u *>(a.k + (int64_t)key * a.kv_stride + kv_head * 128 + chunk * 8);
+  }
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int idx = tid + 256 * p;
+    const int ch = idx >> 3, piece = idx & 7;
+    const int first = min(key0 + piece * 8, a.capacity - 8);
+    t.v[p] = *reinterpret_cast<const v4u *>(a.vt + (int64_t)(kv_head * 128 + ch) * a.capacity + first);
+  }
+}
+
+__device__ __forceinline__ void store_tile(uint8_t *stage, int tid, const TileRegs &t) {
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int idx = tid + 256 * p;
+    *reinterpret_cast<v4u *>(stage + k_addr(idx >> 4, idx & 15)) = t.k[p];
+  }
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int idx = tid + 256 * p;
+    const int ch = idx >> 3, piece = idx & 7;
+    const int g = piece >> 1, half = piece & 1;  // keys 16g + 8*half .. +7
+    uint2 lo, hi;
+    lo.x = t.v[p][0]; lo.y = t.v[p][1];  // keys +0..3 -> chunk 2g
+    hi.x = t.v[p][2]; hi.y = t.v[p][3];  // keys +4..7 -> chunk 2g+1
+    *reinterpret_cast<uint2 *>(stage + v_addr(ch, 2 * g) + 8 * half) = lo;
+    *reinterpret_cast<uint2 *>(stage + v_addr(ch, 2 * g + 1) + 8 * half) = hi;
+  }
+}
+
+__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kStage];
+  // XCD-major renumbering: consecutive workgroups land on XCDs round-robin.
+  int bid = blockIdx.x;
+  const int total = a.q_blocks * a.kv_heads;
+  const int per_xcd = total / kXcds;
+  if (bid < per_xcd * kXcds) bid = (bid % kXcds) * per_xcd + bid / kXcds;
+  const int kv_head = bid / a.q_blocks;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int col = lane & 31, hf = lane >> 5;
+  const int head = kv_head * a.group + wave % a.group;
+  const int q0 = (bid - kv_head * a.q_blocks) * (128 / a.group) + 32 * (wave / a.group);
+
+  // This lane's query (column of S^T): 8 K-steps of 16 channels, 8 per lane half.
+  v8h qf[8];
+  {
+    const int qt = min(q0 + col, a.capacity - 1);
+    const uint16_t *qrow = a.q + (int64_t)qt * a.q_stride + head * 128 + 8 * hf;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) qf[ks] = *reinterpret_cast<const v8h *>(qrow + 16 * ks);
+  }
+
+  v16f o[4];
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[cb][i] = 0.0f;
+  float m_run = -__builtin_inff(), l_run = 0.0f;
+
+  const int tiles = (a.tokens + kKeys - 1) / kKeys;
+  TileRegs regs;
+  load_tile(a, kv_head, 0, tid, regs);
+  store_tile(lds, tid, regs);
+  __syncthreads();
+
+  for (int t = 0; t < tiles; ++t) {
+    const int key0 = t * kKeys;
+    const bool more = t + 1 < tiles;
+    if (more) load_tile(a, kv_head, key0 + kKeys, tid, regs);
+    const uint8_t *stage = lds + (t & 1) * kStage;
+
+    // S^T for 64 keys: two 32-key blocks.
+    v16f s[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[kb][i] = 0.0f;
+      const int row = kb * 32 + col;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const v8h kf = *reinterpret_cast<const v8h *>(stage + k_addr(row, 2 * ks + hf));
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s[kb], 0, 0, 0);
+      }
+    }
+
+    // Online softmax in base 2. s[kb][i] is key key0 + 32kb + 8(i/4) + 4hf + i%4.
+    float mx = -__builtin_inff();
+    const bool ragged = key0 + kKeys > a.tokens;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float v = s[kb][i] * a.scale_log2;
+        if (ragged && key0 + 32 * kb + 8 * (i >> 2) + 4 * hf + (i & 3) >= a.tokens) v = -__builtin_inff();
+        s[kb][i] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    m_run = m_new;
+    float tile_sum = 0.0f;
+    v8h pf[4];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float p = __builtin_amdgcn_exp2f(s[kb][i] - m_new);
+        tile_sum += p;
+        pf[2 * kb + (i >> 3)][i & 7] = (_Float16)p;
+      }
+    l_run = l_run * alpha + tile_sum;
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[cb][i] *= alpha;
+
+    // O^T += V^T P^T over the tile's four 16-key groups.
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+      const int row = cb * 32 + col;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const v8h vf = *reinterpret_cast<const v8h *>(stage + v_addr(row, 2 * g + hf));
+        o[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[g], o[cb], 0, 0, 0);
+      }
+    }
+
+    if (more) store_tile(lds + ((t + 1) & 1) * kStage, tid, regs);
+    __syncthreads();
+  }
+
+  // Row sums: each lane half holds the partial over its keys.
+  const float l = l_run + __shfl_xor(l_run, 32);
+  const int qt = q0 + col;
+  if (qt >= a.rows_out) return;
+  uint16_t *orow = a.out + (int64_t)qt * a.out_stride + head * 128;
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int ch = cb * 32 + 8 * g4 + 4 * hf;
+      uint2 v;
+      v.x = f16_pack2(o[cb][4 * g4] / l, o[cb][4 * g4 + 1] / l);
+      v.y = f16_pack2(o[cb][4 * g4 + 2] / l, o[cb][4 * g4 + 3] / l);
+      *reinterpret_cast<uint2 *>(orow + ch) = v;
+    }
+}
+
+}  // namespace attn
+
+hipError_t launch_rope_qknorm(hipStream_t stream, const RopeLaunch &l) {
+  attn::RopeArgs r;
+  r.qkv = static_cast<const uint16_t *>(l.qkv);
+  r.q_scale = l.q_scale;
+  r.k_scale = l.k_scale;
+  r.cos = l.cos;
+  r.sin = l.sin;
+  r.q_out = static_cast<uint16_t *>(l.q_out);
+  r.k_out = static_cast<uint16_t *>(l.k_out);
+  r.v_out = static_cast<uint16_t *>(l.v_out);
+  r.heads = (int)(l.q_heads + 2 * l.kv_heads);
+  r.items = (uint32_t)(l.tokens * r.heads);
+  r.row_stride = (int)l.row_stride;
+  r.q_heads = (int)l.q_heads;
+  r.kv_heads = (int)l.kv_heads;
+  r.k_offset = (int)l.k_offset;
+  r.eps = l.eps;
+  dim3 grid((r.items + 15) / 16), block(256);
+  hipLaunchKernelGGL(attn::rope_qknorm_kernel, grid, block, 0, stream, r);
+  return hipGetLastError();
+}
+
+hipError_t launch_v_transpose(hipStream_t stream, int64_t rows, int64_t width, int64_t capacity,
+                              const void *x, void *out) {
+  dim3 grid((unsigned)((rows + 63) / 64), (unsigned)((width + 63) / 64)), block(256);
+  hipLaunchKernelGGL(attn::v_transpose_kernel, grid, block, 0, stream, static_cast<const uint16_t *>(x),
+                     static_cast<uint16_t *>(out), (int)rows, (int)width, (int)capacity);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention(hipStream_t stream, const AttentionLaunch &l) {
+  attn::AttnArgs a;
+  a.q = static_cast<const uint16_t *>(l.q);
+  a.k = static_cast<const uint16_t *>(l.k);
+  a.vt = static_cast<const uint16_t *>(l.vt);
+  a.out = static_cast<uint16_t *>(l.out);
+  a.tokens = (int)l.tokens;
+  a.rows_out = (int)l.rows_out;
+  a.capacity = (int)l.capacity;
+  a.q_stride = (int)l.q_stride;
+  a.kv_stride = (int)l.kv_stride;
+  a.out_stride = (int)l.out_stride;
+  a.kv_heads = (int)l.kv_heads;
+  a.group = (int)l.group;
+  a.q_blocks = (int)((l.tokens + 128 / l.group - 1) / (128 / l.group));
+  a.scale_log2 = (float)((double)l.scale * 1.4426950408889634);
+  dim3 grid((unsigned)(a.q_blocks * a.kv_heads)), block(256);
+  hipLaunchKernelGGL(attn::attention_kernel, grid, block, 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace k2w8

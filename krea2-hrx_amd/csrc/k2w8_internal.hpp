@@ -41,6 +41,26 @@ hipError_t configure_gemm_lds();
 hipError_t launch_transport(int direction, hipStream_t stream, int64_t count, const void *x,
                             void *out);
 
+// The attention step (rope_qknorm, V transpose, fp16 GQA attention).
+struct RopeLaunch {
+  const void *qkv = nullptr;
+  const float *q_scale = nullptr, *k_scale = nullptr, *cos = nullptr, *sin = nullptr;
+  void *q_out = nullptr, *k_out = nullptr, *v_out = nullptr;
+  int64_t tokens = 0, row_stride = 0, q_heads = 0, kv_heads = 0, k_offset = 0;
+  float eps = 0.0f;
+};
+hipError_t launch_rope_qknorm(hipStream_t stream, const RopeLaunch &l);
+hipError_t launch_v_transpose(hipStream_t stream, int64_t rows, int64_t width, int64_t capacity,
+                              const void *x, void *out);
+struct AttentionLaunch {
+  const void *q = nullptr, *k = nullptr, *vt = nullptr;
+  void *out = nullptr;
+  int64_t tokens = 0, rows_out = 0, capacity = 0, q_stride = 0, kv_stride = 0, out_stride = 0, kv_heads = 0;
+  int64_t group = 4;  // query heads per key-value head: 1, 2 or 4
+  float scale = 0.0f;
+};
+hipError_t launch_attention(hipStream_t stream, const AttentionLaunch &l);
+
 // Multiprocessor (CU) count of the current device, cached per device ordinal.
 int device_cus();
 

@@ -17,6 +17,7 @@ from ._lib import Internal, InvalidArgument, Krea2Error, Runtime, lib, library_p
 from .ops import (  # noqa: F401
     GemmConfig,
     Quantized,
+    attention_f16,
     gemm_i8,
     gemm_i8_acc,
     gemm_i8_bias,
@@ -27,6 +28,8 @@ from .ops import (  # noqa: F401
     prepare_gated_i8,
     prepare_norm_i8,
     prepare_plain_i8,
+    rope_qknorm_f16,
+    v_transpose,
 )
 
 __all__ = [
@@ -36,6 +39,7 @@ __all__ = [
     "Krea2Error",
     "Quantized",
     "Runtime",
+    "attention_f16",
     "gemm_i8",
     "gemm_i8_acc",
     "gemm_i8_bias",
@@ -48,5 +52,7 @@ __all__ = [
     "prepare_gated_i8",
     "prepare_norm_i8",
     "prepare_plain_i8",
+    "rope_qknorm_f16",
+    "v_transpose",
     "shape",
 ]

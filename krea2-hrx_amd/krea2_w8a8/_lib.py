@@ -55,6 +55,23 @@ class QuantizedCfg(ctypes.Structure):
     _fields_ = [("inputs", ctypes.c_int64), ("outputs", ctypes.c_int64), ("pitch", ctypes.c_int64)]
 
 
+class RopeQknormCfg(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int64) for n in ("row_stride", "q_heads", "kv_heads", "k_offset")] + [
+        ("eps", ctypes.c_float)
+    ]
+
+
+class VTransposeCfg(ctypes.Structure):
+    _fields_ = [("width", ctypes.c_int64), ("row_capacity", ctypes.c_int64)]
+
+
+class AttentionCfg(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int64) for n in (
+        "q_stride", "kv_stride", "out_stride", "tokens", "token_capacity")] + [
+        ("scale", ctypes.c_float)
+    ]
+
+
 class TensorInfo(ctypes.Structure):
     _fields_ = [
         ("dtype", ctypes.c_int32),
@@ -133,6 +150,13 @@ SIGNATURES = {
         ctypes.c_int,
         [_P, ctypes.POINTER(QuantizedCfg), _I64, _P, _P, _P, _P, _P, _P, _P, _P],
     ),
+    "k2w8_rope_qknorm_f16": (
+        ctypes.c_int, [_P, ctypes.POINTER(RopeQknormCfg), _I64, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "k2w8_v_transpose": (ctypes.c_int, [_P, ctypes.POINTER(VTransposeCfg), _I64, _P, _P]),
+    "k2w8_attention_f16": (
+        ctypes.c_int, [_P, ctypes.POINTER(AttentionCfg), _I64, _I64, _P, _P, _P, _P]),
+    "k2w8_attention_f16_grouped": (
+        ctypes.c_int, [_P, ctypes.POINTER(AttentionCfg), _I64, _I64, _I64, _P, _P, _P, _P]),
     "k2w8_checkpoint_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)]),
     "k2w8_checkpoint_close": (None, [_P]),
     "k2w8_checkpoint_block_count": (_I64, [_P]),

@@ -6,6 +6,9 @@ Binding order follows the Loom ``launch(...)`` signatures:
   prepare_gated(attn, gate, q, q_scale)                           kernels/prepare_gated_i8.loom:22
   gemm_i8*(a, w, scale, a_scale, c[, gate])                       kernels/gemm_i8_256.loom:36,
                                                                   kernels/gemm_i8_resid_256.loom:36
+  rope_qknorm(qkv, q_scale, k_scale, cos, sin, q_out, k_out, v_out) kernels/rope_qknorm_f16.loom:24
+  v_transpose(x, out)                                             kernels/native/v_transpose.loom:21
+  attention(q, k, v, out)                                         kernels/attention_gqa_lds_f16_wmma.loom:35
 Configuration keys are the ``config.decl`` names. The runtime scalar (``tokens``
 or ``m``) defaults to the leading dimension of the first operand.
 
@@ -21,12 +24,15 @@ from dataclasses import dataclass
 import torch
 
 from ._lib import (
+    AttentionCfg,
     GemmCfg,
     InvalidArgument,
     PrepareGatedCfg,
     PrepareNormCfg,
     PreparePlainCfg,
     QuantizedCfg,
+    RopeQknormCfg,
+    VTransposeCfg,
     check,
     lib,
 )
@@ -191,6 +197,64 @@ def lora_transport(x, out, *, reverse: int, count=None, stream=None):
     px = _buf(x, "x", src, n)
     po = _buf(out, "out", dst, n)
     check(lib().k2w8_lora_transport(_stream(stream), int(reverse), n, px, po))
+
+
+def rope_qknorm_f16(qkv, q_scale, k_scale, cos, sin, q_out, k_out, v_out, *, row_stride,
+                    q_heads, kv_heads, k_offset, eps, tokens=None, stream=None):
+    """Per-head RMSNorm (multiplier 1 + scale) and rotary embedding of q and k, v copied.
+
+    ``qkv`` f16 [tokens][row_stride]; ``q_scale``/``k_scale`` f32 [128]; ``cos``/``sin``
+    f32 [tokens][128]; ``q_out`` f16 [tokens][q_heads*128]; ``k_out``/``v_out`` f16
+    [tokens][kv_heads*128].
+    """
+    n = _tokens(qkv, tokens)
+    cfg = RopeQknormCfg(row_stride, q_heads, kv_heads, k_offset, eps)
+    args = (
+        _buf(qkv, "qkv", torch.float16, n * row_stride),
+        _buf(q_scale, "q_scale", torch.float32, 128),
+        _buf(k_scale, "k_scale", torch.float32, 128),
+        _buf(cos, "cos", torch.float32, n * 128),
+        _buf(sin, "sin", torch.float32, n * 128),
+        _buf(q_out, "q_out", torch.float16, n * q_heads * 128),
+        _buf(k_out, "k_out", torch.float16, n * kv_heads * 128),
+        _buf(v_out, "v_out", torch.float16, n * kv_heads * 128),
+    )
+    check(lib().k2w8_rope_qknorm_f16(_stream(stream), ctypes.byref(cfg), n, *args))
+
+
+def v_transpose(x, out, *, width, row_capacity, rows=None, stream=None):
+    """f16 ``x`` [rows][width] -> ``out`` [width][row_capacity]; columns past ``rows``
+    are left as they are."""
+    n = _tokens(x, rows)
+    cfg = VTransposeCfg(width, row_capacity)
+    args = (
+        _buf(x, "x", torch.float16, n * width),
+        _buf(out, "out", torch.float16, width * row_capacity),
+    )
+    check(lib().k2w8_v_transpose(_stream(stream), ctypes.byref(cfg), n, *args))
+
+
+def attention_f16(q, k, v, out, *, q_stride, kv_stride, out_stride, tokens, token_capacity, scale,
+                  kv_heads, token_count=None, group=4, stream=None):
+    """Grouped-query attention over ``tokens`` keys, ``group`` query heads per key-value
+    head (4 as in the reference kernel; 1 and 2 are an extension).
+
+    ``q`` f16 [token_capacity][q_stride]; ``k`` f16 [token_capacity][kv_stride]; ``v`` is
+    V^T, f16 [kv_stride][token_capacity]; ``out`` f16 [token_count][out_stride].
+    """
+    n = int(tokens) if token_count is None else int(token_count)
+    cfg = AttentionCfg(q_stride, kv_stride, out_stride, tokens, token_capacity, scale)
+    args = (
+        _buf(q, "q", torch.float16, token_capacity * q_stride),
+        _buf(k, "k", torch.float16, token_capacity * kv_stride),
+        _buf(v, "v", torch.float16, kv_stride * token_capacity),
+        _buf(out, "out", torch.float16, n * out_stride),
+    )
+    if group == 4:
+        check(lib().k2w8_attention_f16(_stream(stream), ctypes.byref(cfg), n, int(kv_heads), *args))
+    else:
+        check(lib().k2w8_attention_f16_grouped(_stream(stream), ctypes.byref(cfg), n, int(kv_heads),
+                                               int(group), *args))
 
 
 @dataclass(frozen=True)

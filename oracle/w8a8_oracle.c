@@ -22,6 +22,14 @@
  *   epilogue_plain    exact KAT src/training/quantized.rs:220
  *   epilogue_resid    tests/quantized.rs:229-243 tolerance + closed form
  *   epilogue_swiglu   tests/quantized.rs:244-255 tolerance (exp unpinned, as above)
+ *   rope_qknorm       tolerance test of tests/quantized.rs:85-166 against an f64 norm,
+ *                     the f32 rotary sum and the exact v copy; the in-wave sum-of-squares
+ *                     order and rsqrt are the Loom compiler's, so bit parity is unpinned
+ *                     (canonical order in ora_head_sum_squares)
+ *   v_transpose       exact: a permutation, checked against numpy's transpose
+ *   attention         tests/quantized.rs:313-380 tolerance against an f64 softmax;
+ *                     the reference's exp and MMA summation order belong to its compiler
+ *                     and hardware: parity is a tolerance, not bits
  */
 #include "w8a8_oracle.h"
 
@@ -404,5 +412,126 @@ void ora_gemm_i8(int64_t m, int64_t n, int64_t k_size, int64_t k_stride, const i
                 c_f16[r * n + c] = ora_f16_from_f32(plain_value(s, w_scale[c], a_scale[r]));
             }
         }
+    }
+}
+
+/* ---- The attention step ------------------------------------------------------ */
+
+/* Sum of squares of one 128-channel head in this build's canonical order: sixteen
+ * partials of eight channels, each ((x0^2+x1^2)+(x2^2+x3^2))+((x4^2+x5^2)+(x6^2+x7^2)),
+ * combined by a butterfly over partial offsets 1, 2, 4, 8 (pairwise tree in index
+ * order). The reference (kernels/rope_qknorm_f16.loom:109-113) reduces four channels per
+ * lane and then across its wave in an order its compiler chooses. */
+float ora_head_sum_squares(const uint16_t *h) {
+    float part[16];
+    for (int j = 0; j < 16; ++j) {
+        float x[8];
+        for (int e = 0; e < 8; ++e) x[e] = ora_f16_to_f32(h[8 * j + e]);
+        part[j] = ((x[0] * x[0] + x[1] * x[1]) + (x[2] * x[2] + x[3] * x[3])) +
+                  ((x[4] * x[4] + x[5] * x[5]) + (x[6] * x[6] + x[7] * x[7]));
+    }
+    for (int d = 1; d < 16; d <<= 1)
+        for (int j = 0; j < 16; j += 2 * d) part[j] = part[j] + part[j + d];
+    return part[0];
+}
+
+/* kernels/rope_qknorm_f16.loom:73-154: x = bf16((h * r) * (1 + scale[c])) with
+ * r = 1/sqrt(ss/128 + eps); pairs rotate as (x0 cos - x1 sin, x1 cos + x0 sin), rounded
+ * to bf16 and stored as f16 (:128-146); v heads are copied (:90-94). */
+void ora_rope_qknorm_f16(int64_t tokens, int64_t row_stride, int64_t q_heads, int64_t kv_heads,
+                         int64_t k_offset, float eps, const uint16_t *qkv, const float *q_scale,
+                         const float *k_scale, const float *cos_t, const float *sin_t,
+                         uint16_t *q_out, uint16_t *k_out, uint16_t *v_out) {
+    const int64_t heads = q_heads + 2 * kv_heads;
+#pragma omp parallel for schedule(static)
+    for (int64_t item = 0; item < tokens * heads; ++item) {
+        const int64_t t = item / heads, head = item % heads;
+        const uint16_t *row = qkv + t * row_stride;
+        if (head >= q_heads + kv_heads) {
+            const int64_t vh = head - q_heads - kv_heads;
+            memcpy(v_out + (t * kv_heads + vh) * 128, row + k_offset + (kv_heads + vh) * 128, 256);
+            continue;
+        }
+        const int is_q = head < q_heads;
+        const int64_t kh = head - q_heads;
+        const uint16_t *h = row + (is_q ? head * 128 : k_offset + kh * 128);
+        const float *scale = is_q ? q_scale : k_scale;
+        const float ss = ora_head_sum_squares(h);
+        /* reference: rsqrtf (compiler-defined); canonical: correctly rounded 1/sqrt */
+        const float rinv = 1.0f / sqrtf(ss * 0.0078125f + eps);
+        float x[128];
+        for (int c = 0; c < 128; ++c)
+            x[c] = ora_bf16_to_f32(ora_bf16_from_f32((ora_f16_to_f32(h[c]) * rinv) * (scale[c] + 1.0f)));
+        uint16_t *dst = is_q ? q_out + (t * q_heads + head) * 128 : k_out + (t * kv_heads + kh) * 128;
+        const float *cs = cos_t + t * 128, *sn = sin_t + t * 128;
+        for (int c = 0; c < 128; c += 2) {
+            const float a = x[c] * cs[c] - x[c + 1] * sn[c];
+            const float b = x[c + 1] * cs[c + 1] + x[c] * sn[c + 1];
+            dst[c] = ora_f16_from_f32(ora_bf16_to_f32(ora_bf16_from_f32(a)));
+            dst[c + 1] = ora_f16_from_f32(ora_bf16_to_f32(ora_bf16_from_f32(b)));
+        }
+    }
+}
+
+/* kernels/native/v_transpose.loom:48-88 */
+void ora_v_transpose(int64_t rows, int64_t width, int64_t capacity, const uint16_t *x,
+                     uint16_t *out) {
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < width; ++c) out[c * capacity + r] = x[r * width + c];
+}
+
+/* kernels/attention_gqa_lds_f16_wmma.loom:170-335: for each query row and head, scores
+ * s_j = scale * (q . k_j) with f32 products of f16 values, keys j >= tokens excluded;
+ * per key tile the running max m moves to max(m, tile max), the running sum and the
+ * accumulators are scaled by exp(m_old - m_new), each weight w_j = exp(s_j - m_new) is
+ * added to the sum in f32 and, rounded to f16, multiplies v_j into the accumulators;
+ * out = f16(acc / sum) (:337-379). */
+void ora_attention_f16(int64_t tokens, int64_t rows_out, int64_t capacity, int64_t q_stride,
+                       int64_t kv_stride, int64_t out_stride, int64_t kv_heads, int64_t group,
+                       float scale, int64_t key_tile, const uint16_t *q, const uint16_t *k,
+                       const uint16_t *vt, uint16_t *out, int threads) {
+    const int nt = threads > 0 ? threads : ora_max_threads();
+    const int64_t heads = group * kv_heads;
+    const int64_t rows = rows_out < tokens ? rows_out : tokens;
+#pragma omp parallel num_threads(nt)
+    {
+        float *s = malloc(sizeof(float) * (size_t)key_tile);
+#pragma omp for schedule(dynamic, 1) collapse(2)
+        for (int64_t h = 0; h < heads; ++h)
+            for (int64_t t = 0; t < rows; ++t) {
+                const int64_t kvh = h / group;
+                float qv[128], acc[128];
+                for (int c = 0; c < 128; ++c) {
+                    qv[c] = ora_f16_to_f32(q[t * q_stride + h * 128 + c]);
+                    acc[c] = 0.0f;
+                }
+                float m = -INFINITY, sum = 0.0f;
+                for (int64_t j0 = 0; j0 < tokens; j0 += key_tile) {
+                    const int64_t n = tokens - j0 < key_tile ? tokens - j0 : key_tile;
+                    float tmax = -INFINITY;
+                    for (int64_t j = 0; j < n; ++j) {
+                        const uint16_t *kr = k + (j0 + j) * kv_stride + kvh * 128;
+                        float dot = 0.0f;
+                        for (int c = 0; c < 128; ++c) dot += qv[c] * ora_f16_to_f32(kr[c]);
+                        s[j] = dot * scale;
+                        if (s[j] > tmax) tmax = s[j];
+                    }
+                    const float m_new = m > tmax ? m : tmax;
+                    const float alpha = expf(m - m_new);
+                    sum *= alpha;
+                    for (int c = 0; c < 128; ++c) acc[c] *= alpha;
+                    for (int64_t j = 0; j < n; ++j) {
+                        const float w = expf(s[j] - m_new);
+                        sum += w;
+                        const float w16 = ora_f16_to_f32(ora_f16_from_f32(w));
+                        for (int c = 0; c < 128; ++c)
+                            acc[c] += w16 * ora_f16_to_f32(vt[(kvh * 128 + c) * capacity + j0 + j]);
+                    }
+                    m = m_new;
+                }
+                for (int c = 0; c < 128; ++c)
+                    out[t * out_stride + h * 128 + c] = ora_f16_from_f32(acc[c] / sum);
+            }
+        free(s);
     }
 }

@@ -68,6 +68,32 @@ void ora_gemm_i8(int64_t m, int64_t n, int64_t k_size, int64_t k_stride, const i
                  const int8_t *w, const float *w_scale, const float *a_scale, uint16_t *c_f16,
                  int threads);
 
+/* The attention step of a block (src/session/mod.rs:714-755). */
+
+/* kernels/rope_qknorm_f16.loom: per-head RMSNorm + rotary embedding of q and k, v copied.
+ * qkv f16 [tokens][row_stride] -> q_out [tokens][q_heads*128], k_out/v_out
+ * [tokens][kv_heads*128]. The per-head sum of squares runs in this build's canonical
+ * order (see ora_head_sum_squares). */
+void ora_rope_qknorm_f16(int64_t tokens, int64_t row_stride, int64_t q_heads, int64_t kv_heads,
+                         int64_t k_offset, float eps, const uint16_t *qkv, const float *q_scale,
+                         const float *k_scale, const float *cos_t, const float *sin_t,
+                         uint16_t *q_out, uint16_t *k_out, uint16_t *v_out);
+float ora_head_sum_squares(const uint16_t *h_head);
+
+/* kernels/native/v_transpose.loom: x [rows][width] -> out [width][capacity]; columns
+ * at or past rows untouched. */
+void ora_v_transpose(int64_t rows, int64_t width, int64_t capacity, const uint16_t *x,
+                     uint16_t *out);
+
+/* kernels/attention_gqa_lds_f16_wmma.loom: grouped-query attention, query head h on
+ * kv head h/group (group 4 in the reference kernel), online softmax over key tiles of `key_tile` keys (16 in the reference
+ * kernel), weights rounded to f16 for the PV product. vt is V^T [kv_stride][capacity].
+ * Writes out rows < rows_out. */
+void ora_attention_f16(int64_t tokens, int64_t rows_out, int64_t capacity, int64_t q_stride,
+                       int64_t kv_stride, int64_t out_stride, int64_t kv_heads, int64_t group,
+                       float scale, int64_t key_tile, const uint16_t *q, const uint16_t *k,
+                       const uint16_t *vt, uint16_t *out, int threads);
+
 int ora_max_threads(void);
 
 #ifdef __cplusplus

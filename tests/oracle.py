@@ -48,6 +48,10 @@ def lib() -> ctypes.CDLL:
             "ora_epilogue_bias": (None, [I, I, P, P, P, P, P]),
             "ora_gemm_i8": (None, [I, I, I, I, P, P, P, P, P, ctypes.c_int]),
             "ora_max_threads": (ctypes.c_int, []),
+            "ora_rope_qknorm_f16": (None, [I, I, I, I, I, F, P, P, P, P, P, P, P, P]),
+            "ora_head_sum_squares": (F, [P]),
+            "ora_v_transpose": (None, [I, I, I, P, P]),
+            "ora_attention_f16": (None, [I, I, I, I, I, I, I, I, F, I, P, P, P, P, ctypes.c_int]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name)
@@ -178,3 +182,44 @@ def gemm_i8(a, w, m, n, k_size, k_stride, w_scale, a_scale, threads=0):
 
 def max_threads() -> int:
     return int(lib().ora_max_threads())
+
+
+def rope_qknorm(qkv_f16_bits, q_scale, k_scale, cos, sin, *, row_stride, q_heads, kv_heads,
+                k_offset, eps):
+    """(q_out, k_out, v_out) as f16 bit patterns, [tokens][heads*128]."""
+    qkv = np.ascontiguousarray(qkv_f16_bits, np.uint16)
+    tokens = qkv.size // row_stride
+    q_out = np.empty((tokens, q_heads * 128), np.uint16)
+    k_out = np.empty((tokens, kv_heads * 128), np.uint16)
+    v_out = np.empty((tokens, kv_heads * 128), np.uint16)
+    lib().ora_rope_qknorm_f16(tokens, row_stride, q_heads, kv_heads, k_offset, eps, _p(qkv),
+                              _p(np.ascontiguousarray(q_scale, np.float32)),
+                              _p(np.ascontiguousarray(k_scale, np.float32)),
+                              _p(np.ascontiguousarray(cos, np.float32)),
+                              _p(np.ascontiguousarray(sin, np.float32)), _p(q_out), _p(k_out),
+                              _p(v_out))
+    return q_out, k_out, v_out
+
+
+def head_sum_squares(h_f16_bits) -> float:
+    return float(lib().ora_head_sum_squares(_p(np.ascontiguousarray(h_f16_bits, np.uint16))))
+
+
+def v_transpose(x_f16_bits, rows, width, capacity, out=None):
+    x = np.ascontiguousarray(x_f16_bits, np.uint16)
+    if out is None:
+        out = np.zeros((width, capacity), np.uint16)
+    lib().ora_v_transpose(rows, width, capacity, _p(x), _p(out))
+    return out
+
+
+def attention(q_bits, k_bits, vt_bits, *, tokens, capacity, q_stride, kv_stride, out_stride,
+              kv_heads, scale, group=4, key_tile=16, rows_out=None, threads=0):
+    """f16 bit patterns [rows_out][out_stride] (columns past 4*kv_heads*128 zero)."""
+    rows = tokens if rows_out is None else rows_out
+    out = np.zeros((rows, out_stride), np.uint16)
+    lib().ora_attention_f16(tokens, rows, capacity, q_stride, kv_stride, out_stride, kv_heads,
+                            group, scale, key_tile, _p(np.ascontiguousarray(q_bits, np.uint16)),
+                            _p(np.ascontiguousarray(k_bits, np.uint16)),
+                            _p(np.ascontiguousarray(vt_bits, np.uint16)), _p(out), threads)
+    return out
