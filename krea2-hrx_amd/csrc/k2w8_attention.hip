@@ -152,11 +152,14 @@ __global__ __launch_bounds__(256) void v_transpose_kernel(const uint16_t *x, uin
 // 256 threads: wave w computes query head kv_head*group + w % group for the 32 query
 // tokens starting at the block's first + 32 * (w / group).
 //
-// LDS, two stages of 32 KiB:
-//   K tile   [64 keys][128 ch] f16, 256-byte rows, 16-byte chunk c of row r at c ^ (r & 15)
-//   V^T tile [128 ch][64 keys] f16, 128-byte rows, chunk c of row r at c ^ ((r >> 1) & 7);
-//            within each 16-key group, chunk 2g holds keys {0-3, 8-11} and chunk 2g+1
-//            keys {4-7, 12-15}: the key order of a lane half's probability registers.
+// LDS, two stages of 32 KiB, filled by global_load_lds_dwordx4 (no staging registers):
+//   K tile   [64 rows][128 ch] f16, 256-byte rows; row r holds key perm(r), which swaps
+//            bits 2 and 3 of r, so that a lane half's eight score registers of a 16-key
+//            group are eight consecutive keys. 16-byte chunk c of row r at c ^ (r & 15).
+//   V^T tile [128 ch][64 keys] f16, 128-byte rows in key order; chunk c of row r at
+//            c ^ ((r >> 1) & 7).
+// Two workgroups share a CU (LDS 64 KiB and at most 256 registers per lane each), so a
+// SIMD interleaves one wave's softmax with another's MFMAs.
 // ---------------------------------------------------------------------------------
 struct AttnArgs {
   const uint16_t *q, *k, *vt;
@@ -168,52 +171,25 @@ struct AttnArgs {
 constexpr int kKeys = 64;
 constexpr int kStage = 2 * 16384;
 
+__device__ __forceinline__ int key_of_row(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 __device__ __forceinline__ int k_addr(int row, int chunk) { return row * 256 + ((chunk ^ (row & 15)) << 4); }
 __device__ __forceinline__ int v_addr(int row, int chunk) {
   return 16384 + row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4);
 }
 
-struct TileRegs {
-  v4u k[4], v[4];
-};
-
-__device__ __forceinline__ void load_tile(const AttnArgs &a, int kv_head, int key0, int tid, TileRegs &t) {
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const int idx = tid + 256 * p;
-    const int row = idx >> 4, chunk = idx & 15;
-    const int key = min(key0 + row, a.capacity - 1);
-    t.k[p] = *reinterpret_cast<const v4u *>(a.k + (int64_t)key * a.kv_stride + kv_head * 128 + chunk * 8);
-  }
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const int idx = tid + 256 * p;
-    const int ch = idx >> 3, piece = idx & 7;
-    const int first = min(key0 + piece * 8, a.capacity - 8);
-    t.v[p] = *reinterpret_cast<const v4u *>(a.vt + (int64_t)(kv_head * 128 + ch) * a.capacity + first);
-  }
+__device__ __forceinline__ const void *uniform_ptr(const void *p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<const void *>(((uint64_t)hi << 32) | lo);
 }
 
-__device__ __forceinline__ void store_tile(uint8_t *stage, int tid, const TileRegs &t) {
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const int idx = tid + 256 * p;
-    *reinterpret_cast<v4u *>(stage + k_addr(idx >> 4, idx & 15)) = t.k[p];
-  }
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const int idx = tid + 256 * p;
-    const int ch = idx >> 3, piece = idx & 7;
-    const int g = piece >> 1, half = piece & 1;  // keys 16g + 8*half .. +7
-    uint2 lo, hi;
-    lo.x = t.v[p][0]; lo.y = t.v[p][1];  // keys +0..3 -> chunk 2g
-    hi.x = t.v[p][2]; hi.y = t.v[p][3];  // keys +4..7 -> chunk 2g+1
-    *reinterpret_cast<uint2 *>(stage + v_addr(ch, 2 * g) + 8 * half) = lo;
-    *reinterpret_cast<uint2 *>(stage + v_addr(ch, 2 * g + 1) + 8 * half) = hi;
-  }
+// Lane l writes LDS bytes [lds + 16 l, +16) from global base + voff (bytes).
+__device__ __forceinline__ void dma16(uint32_t lds, const void *base, uint32_t voff) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(uniform_ptr(base)), "{m0}"(lds) : "memory");
 }
 
-__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kStage];
   // XCD-major renumbering: consecutive workgroups land on XCDs round-robin.
   int bid = blockIdx.x;
@@ -222,10 +198,42 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
   if (bid < per_xcd * kXcds) bid = (bid % kXcds) * per_xcd + bid / kXcds;
   const int kv_head = bid / a.q_blocks;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int col = lane & 31, hf = lane >> 5;
   const int head = kv_head * a.group + wave % a.group;
   const int q0 = (bid - kv_head * a.q_blocks) * (128 / a.group) + 32 * (wave / a.group);
+
+  // Transfers of one tile: wave w fills K rows 16w..16w+15 and V^T rows 32w..32w+31,
+  // four 1 KiB instructions each. Offsets relative to the tile's first key.
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+  int k_row[4], v_row[4], k_col[4], v_key[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 16 * wave + 4 * j + (lane >> 4);
+    k_row[j] = key_of_row(r);
+    k_col[j] = ((lane & 15) ^ (r & 15)) * 8;
+    const int vr = 32 * wave + 8 * j + (lane >> 3);
+    v_row[j] = vr;
+    v_key[j] = ((lane & 7) ^ ((vr >> 1) & 7)) * 8;
+  }
+  const uint16_t *k_head = a.k + kv_head * 128;
+  const uint16_t *v_head = a.vt + (int64_t)kv_head * 128 * a.capacity;
+  auto issue = [&](int t) {
+    const int key0 = t * kKeys;
+    const uint32_t so = lds0 + (t & 1) * kStage;
+    const uint16_t *kb = k_head + (int64_t)key0 * a.kv_stride;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int key = min(key0 + k_row[j], a.capacity - 1) - key0;
+      dma16(so + (4 * wave + j) * 1024, kb, (uint32_t)(key * a.kv_stride + k_col[j]) * 2u);
+    }
+    const uint16_t *vb = v_head + key0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int first = min(key0 + v_key[j], a.capacity - 8) - key0;
+      dma16(so + 16384 + (4 * wave + j) * 1024, vb, (uint32_t)(v_row[j] * a.capacity + first) * 2u);
+    }
+  };
 
   // This lane's query (column of S^T): 8 K-steps of 16 channels, 8 per lane half.
   v8h qf[8];
@@ -242,20 +250,19 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[cb][i] = 0.0f;
   float m_run = -__builtin_inff(), l_run = 0.0f;
+  const float c = a.scale_log2;
 
   const int tiles = (a.tokens + kKeys - 1) / kKeys;
-  TileRegs regs;
-  load_tile(a, kv_head, 0, tid, regs);
-  store_tile(lds, tid, regs);
-  __syncthreads();
-
+  issue(0);
   for (int t = 0; t < tiles; ++t) {
-    const int key0 = t * kKeys;
-    const bool more = t + 1 < tiles;
-    if (more) load_tile(a, kv_head, key0 + kKeys, tid, regs);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    if (t + 1 < tiles) issue(t + 1);
     const uint8_t *stage = lds + (t & 1) * kStage;
+    const int key0 = t * kKeys;
 
-    // S^T for 64 keys: two 32-key blocks.
+    // S^T for 64 keys: two 32-row blocks. s[kb][i] is key
+    // key0 + 32kb + 16(i/8) + 8hf + i%8.
     v16f s[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -269,37 +276,51 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
       }
     }
 
-    // Online softmax in base 2. s[kb][i] is key key0 + 32kb + 8(i/4) + 4hf + i%4.
-    float mx = -__builtin_inff();
-    const bool ragged = key0 + kKeys > a.tokens;
+    // Online softmax in base 2, on raw scores scaled inside the exponent.
+    if (key0 + kKeys > a.tokens) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float v = s[kb][i] * a.scale_log2;
-        if (ragged && key0 + 32 * kb + 8 * (i >> 2) + 4 * hf + (i & 3) >= a.tokens) v = -__builtin_inff();
-        s[kb][i] = v;
-        mx = fmaxf(mx, v);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
+        for (int i = 0; i < 16; ++i)
+          if (key0 + 32 * kb + 16 * (i >> 3) + 8 * hf + (i & 7) >= a.tokens) s[kb][i] = -__builtin_inff();
+    }
+    float mx[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const v16f &sv = s[g >> 1];
+      const int b = (g & 1) * 8;
+      mx[g] = fmaxf(fmaxf(fmaxf(sv[b], sv[b + 1]), fmaxf(sv[b + 2], sv[b + 3])),
+                    fmaxf(fmaxf(sv[b + 4], sv[b + 5]), fmaxf(sv[b + 6], sv[b + 7])));
+    }
+    float m_tile = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
+    m_tile = fmaxf(m_tile, __shfl_xor(m_tile, 32)) * c;
+    const float m_new = fmaxf(m_run, m_tile);
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
     m_run = m_new;
-    float tile_sum = 0.0f;
+    float part[4];
     v8h pf[4];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int g = 0; g < 4; ++g) {
+      const v16f &sv = s[g >> 1];
+      const int b = (g & 1) * 8;
+      float p[8];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float p = __builtin_amdgcn_exp2f(s[kb][i] - m_new);
-        tile_sum += p;
-        pf[2 * kb + (i >> 3)][i & 7] = (_Float16)p;
-      }
-    l_run = l_run * alpha + tile_sum;
+      for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[b + e], c, -m_new));
+      part[g] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+      typedef uint32_t v4u_ __attribute__((ext_vector_type(4)));
+      v4u_ packed;
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
+      for (int e = 0; e < 4; ++e) packed[e] = f16_pack2(p[2 * e], p[2 * e + 1]);
+      pf[g] = __builtin_bit_cast(v8h, packed);
+    }
+    l_run = l_run * alpha + ((part[0] + part[1]) + (part[2] + part[3]));
+    // Rescale only when some query's maximum moved (alpha == 1 leaves o as it is).
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) o[cb][i] *= alpha;
+      for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[cb][i] *= alpha;
+    }
 
     // O^T += V^T P^T over the tile's four 16-key groups.
 #pragma unroll
@@ -311,13 +332,10 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
         o[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[g], o[cb], 0, 0, 0);
       }
     }
-
-    if (more) store_tile(lds + ((t + 1) & 1) * kStage, tid, regs);
-    __syncthreads();
   }
 
   // Row sums: each lane half holds the partial over its keys.
-  const float l = l_run + __shfl_xor(l_run, 32);
+  const float inv = 1.0f / (l_run + __shfl_xor(l_run, 32));
   const int qt = q0 + col;
   if (qt >= a.rows_out) return;
   uint16_t *orow = a.out + (int64_t)qt * a.out_stride + head * 128;
@@ -327,8 +345,8 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     for (int g4 = 0; g4 < 4; ++g4) {
       const int ch = cb * 32 + 8 * g4 + 4 * hf;
       uint2 v;
-      v.x = f16_pack2(o[cb][4 * g4] / l, o[cb][4 * g4 + 1] / l);
-      v.y = f16_pack2(o[cb][4 * g4 + 2] / l, o[cb][4 * g4 + 3] / l);
+      v.x = f16_pack2(o[cb][4 * g4] * inv, o[cb][4 * g4 + 1] * inv);
+      v.y = f16_pack2(o[cb][4 * g4 + 2] * inv, o[cb][4 * g4 + 3] * inv);
       *reinterpret_cast<uint2 *>(orow + ch) = v;
     }
 }
