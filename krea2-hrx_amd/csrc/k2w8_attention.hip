@@ -189,6 +189,20 @@ __device__ __forceinline__ void dma16(uint32_t lds, const void *base, uint32_t v
   asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(uniform_ptr(base)), "{m0}"(lds) : "memory");
 }
 
+__device__ __forceinline__ float max3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+// The value lane l ^ 32 holds. v_permlane32_swap exchanges lanes 32-63 of its first
+// operand with lanes 0-31 of its second: with x in both, the first result holds
+// x[l - 32] in the upper half and the second x[l + 32] in the lower half.
+__device__ __forceinline__ float across_halves(float x, int hf) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(hf ? r[0] : r[1]);
+}
+
 __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kStage];
   // XCD-major renumbering: consecutive workgroups land on XCDs round-robin.
@@ -204,34 +218,43 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
   const int q0 = (bid - kv_head * a.q_blocks) * (128 / a.group) + 32 * (wave / a.group);
 
   // Transfers of one tile: wave w fills K rows 16w..16w+15 and V^T rows 32w..32w+31,
-  // four 1 KiB instructions each. Offsets relative to the tile's first key.
+  // four 1 KiB instructions each; byte offsets from the tile's first key.
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
-  int k_row[4], v_row[4], k_col[4], v_key[4];
+  int k_row[4], v_key[4];
+  uint32_t k_off[4], v_off[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int r = 16 * wave + 4 * j + (lane >> 4);
     k_row[j] = key_of_row(r);
-    k_col[j] = ((lane & 15) ^ (r & 15)) * 8;
+    const int k_col = ((lane & 15) ^ (r & 15)) * 8;
+    k_off[j] = (uint32_t)(k_row[j] * a.kv_stride + k_col) * 2u;
     const int vr = 32 * wave + 8 * j + (lane >> 3);
-    v_row[j] = vr;
     v_key[j] = ((lane & 7) ^ ((vr >> 1) & 7)) * 8;
+    v_off[j] = (uint32_t)(vr * a.capacity + v_key[j]) * 2u;
   }
   const uint16_t *k_head = a.k + kv_head * 128;
   const uint16_t *v_head = a.vt + (int64_t)kv_head * 128 * a.capacity;
-  auto issue = [&](int t) {
+  const int tiles = (a.tokens + kKeys - 1) / kKeys;
+  auto issue = [&](int t, uint32_t so) __attribute__((always_inline)) {
     const int key0 = t * kKeys;
-    const uint32_t so = lds0 + (t & 1) * kStage;
     const uint16_t *kb = k_head + (int64_t)key0 * a.kv_stride;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int key = min(key0 + k_row[j], a.capacity - 1) - key0;
-      dma16(so + (4 * wave + j) * 1024, kb, (uint32_t)(key * a.kv_stride + k_col[j]) * 2u);
-    }
     const uint16_t *vb = v_head + key0;
+    if (key0 + kKeys <= a.capacity) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int first = min(key0 + v_key[j], a.capacity - 8) - key0;
-      dma16(so + 16384 + (4 * wave + j) * 1024, vb, (uint32_t)(v_row[j] * a.capacity + first) * 2u);
+      for (int j = 0; j < 4; ++j) dma16(so + (4 * wave + j) * 1024, kb, k_off[j]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dma16(so + 16384 + (4 * wave + j) * 1024, vb, v_off[j]);
+    } else {  // the last tile may reach past the buffers' rows: clamp (those keys are masked)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = min(key0 + k_row[j], a.capacity - 1) - key0;
+        dma16(so + (4 * wave + j) * 1024, kb, k_off[j] + (uint32_t)((key - k_row[j]) * a.kv_stride) * 2u);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int first = min(key0 + v_key[j], a.capacity - 8) - key0;
+        dma16(so + 16384 + (4 * wave + j) * 1024, vb, v_off[j] + (uint32_t)(first - v_key[j]) * 2u);
+      }
     }
   };
 
@@ -251,14 +274,21 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
     for (int i = 0; i < 16; ++i) o[cb][i] = 0.0f;
   float m_run = -__builtin_inff(), l_run = 0.0f;
   const float c = a.scale_log2;
+  // Per-lane LDS byte offsets within a stage of the K and V^T fragment rows.
+  int k_frag[8], v_frag[16];
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) k_frag[ks] = k_addr(col, 2 * ks + hf);  // row kb*32 + col: +8192*kb
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) v_frag[cb * 4 + g] = v_addr(cb * 32 + col, 2 * g + hf);
 
-  const int tiles = (a.tokens + kKeys - 1) / kKeys;
-  issue(0);
-  for (int t = 0; t < tiles; ++t) {
+  // One tile on a stage whose offset is a compile-time constant at each call.
+  auto step = [&](int t, const int stage_off) __attribute__((always_inline)) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
-    if (t + 1 < tiles) issue(t + 1);
-    const uint8_t *stage = lds + (t & 1) * kStage;
+    if (t + 1 < tiles) issue(t + 1, lds0 + (stage_off ^ kStage));
+    const uint8_t *stage = lds + stage_off;
     const int key0 = t * kKeys;
 
     // S^T for 64 keys: two 32-row blocks. s[kb][i] is key
@@ -268,10 +298,9 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) s[kb][i] = 0.0f;
-      const int row = kb * 32 + col;
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) {
-        const v8h kf = *reinterpret_cast<const v8h *>(stage + k_addr(row, 2 * ks + hf));
+        const v8h kf = *reinterpret_cast<const v8h *>(stage + kb * 8192 + k_frag[ks]);
         s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s[kb], 0, 0, 0);
       }
     }
@@ -289,11 +318,11 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
     for (int g = 0; g < 4; ++g) {
       const v16f &sv = s[g >> 1];
       const int b = (g & 1) * 8;
-      mx[g] = fmaxf(fmaxf(fmaxf(sv[b], sv[b + 1]), fmaxf(sv[b + 2], sv[b + 3])),
-                    fmaxf(fmaxf(sv[b + 4], sv[b + 5]), fmaxf(sv[b + 6], sv[b + 7])));
+      mx[g] = max3(max3(max3(sv[b], sv[b + 1], sv[b + 2]), sv[b + 3], sv[b + 4]),
+                   max3(sv[b + 5], sv[b + 6], sv[b + 7]), sv[b]);
     }
-    float m_tile = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
-    m_tile = fmaxf(m_tile, __shfl_xor(m_tile, 32)) * c;
+    float m_tile = max3(max3(mx[0], mx[1], mx[2]), mx[3], mx[3]);
+    m_tile = max3(m_tile, across_halves(m_tile, hf), m_tile) * c;
     const float m_new = fmaxf(m_run, m_tile);
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
     m_run = m_new;
@@ -307,8 +336,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[b + e], c, -m_new));
       part[g] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-      typedef uint32_t v4u_ __attribute__((ext_vector_type(4)));
-      v4u_ packed;
+      v4u packed;
 #pragma unroll
       for (int e = 0; e < 4; ++e) packed[e] = f16_pack2(p[2 * e], p[2 * e + 1]);
       pf[g] = __builtin_bit_cast(v8h, packed);
@@ -324,18 +352,22 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
 
     // O^T += V^T P^T over the tile's four 16-key groups.
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
-      const int row = cb * 32 + col;
+    for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const v8h vf = *reinterpret_cast<const v8h *>(stage + v_addr(row, 2 * g + hf));
+        const v8h vf = *reinterpret_cast<const v8h *>(stage + v_frag[cb * 4 + g]);
         o[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[g], o[cb], 0, 0, 0);
       }
-    }
+  };
+
+  issue(0, lds0);
+  for (int t = 0; t < tiles; t += 2) {
+    step(t, 0);
+    if (t + 1 < tiles) step(t + 1, kStage);
   }
 
   // Row sums: each lane half holds the partial over its keys.
-  const float inv = 1.0f / (l_run + __shfl_xor(l_run, 32));
+  const float inv = 1.0f / (l_run + across_halves(l_run, hf));
   const int qt = q0 + col;
   if (qt >= a.rows_out) return;
   uint16_t *orow = a.out + (int64_t)qt * a.out_stride + head * 128;
