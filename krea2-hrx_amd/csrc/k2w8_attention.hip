@@ -265,6 +265,10 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
     const uint16_t *qrow = a.q + (int64_t)qt * a.q_stride + head * 128 + 8 * hf;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) qf[ks] = *reinterpret_cast<const v8h *>(qrow + 16 * ks);
+    // Consume the loads here: a first use inside the tile loop would make the compiler
+    // wait on the loop's later transfers (vmcnt counts both) in every iteration.
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) asm volatile("" ::"v"(qf[ks]));
   }
 
   v16f o[4];
@@ -293,17 +297,19 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
 
     // S^T for 64 keys: two 32-row blocks. s[kb][i] is key
     // key0 + 32kb + 16(i/8) + 8hf + i%8.
+    // The two blocks' MFMA chains alternate, so no MFMA waits on the one before it.
     v16f s[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) s[kb][i] = 0.0f;
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
         const v8h kf = *reinterpret_cast<const v8h *>(stage + kb * 8192 + k_frag[ks]);
         s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s[kb], 0, 0, 0);
       }
-    }
 
     // Online softmax in base 2, on raw scores scaled inside the exponent.
     if (key0 + kKeys > a.tokens) {
@@ -350,11 +356,11 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
         for (int i = 0; i < 16; ++i) o[cb][i] *= alpha;
     }
 
-    // O^T += V^T P^T over the tile's four 16-key groups.
+    // O^T += V^T P^T over the tile's four 16-key groups (four independent chains).
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
+    for (int g = 0; g < 4; ++g)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
+      for (int cb = 0; cb < 4; ++cb) {
         const v8h vf = *reinterpret_cast<const v8h *>(stage + v_frag[cb * 4 + g]);
         o[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[g], o[cb], 0, 0, 0);
       }
