@@ -32,7 +32,7 @@ extern "C" {
 #define K2W8_RUNTIME (-3)          /* Error::Runtime (a hipError_t) */
 
 /* The ABI revision this header describes. */
-#define K2W8_ABI_VERSION 1
+#define K2W8_ABI_VERSION 2
 int k2w8_abi_version(void);
 
 /* Message of the last failure on the calling thread ("" after success). */
@@ -362,6 +362,7 @@ typedef struct k2w8_block_weights {
   const int8_t *gu_q;   const float *gu_s;
   const int8_t *down_q; const float *down_s;
   const float *prenorm; const float *postnorm;
+  const float *qnorm;   const float *knorm;  /* f32 [128]: rope_qknorm's q_scale, k_scale */
 } k2w8_block_weights;
 
 /* The session's workspaces (src/session/mod.rs:321-340), owned by the caller. */
@@ -373,12 +374,28 @@ typedef struct k2w8_block_buffers {
   void *attn_gu;     /* f16 [tokens][max(hidden, inter)]: attention output, then SwiGLU output */
   const float *mods; /* f32 [layers][6][hidden]: prescale, preshift, pregate, postscale,
                         postshift, postgate (src/session/mod.rs:133-138) */
+  /* The attention step's workspaces (src/session/mod.rs:327-341), capacity =
+   * k2w8_shape_capacity(tokens), kv = (gate_offset - hidden) / 2 columns of k and of v.
+   * With q NULL the block runs its W8A8 stages only and the caller leaves the attention
+   * output in attn_gu between k2w8_block_pre_attention and k2w8_block_post_attention. */
+  void *q;          /* f16 [capacity][hidden], rows past tokens zero */
+  void *k;          /* f16 [capacity][kv], rows past tokens zero */
+  void *v;          /* f16 [capacity][kv] */
+  void *vt;         /* f16 [kv][capacity], columns past tokens zero */
+  const float *cos; /* f32 [tokens][128] */
+  const float *sin; /* f32 [tokens][128] */
 } k2w8_block_buffers;
 
 /* Session::block (src/session/mod.rs:671-711), up to the attention: prepare_norm_i8
  * with the block's prenorm and modulation rows 0/1, then gemm_qkvg into `fused`. */
 int k2w8_block_pre_attention(void *stream, const k2w8_block_cfg *cfg, int64_t index,
                              const k2w8_block_weights *weights, const k2w8_block_buffers *buffers);
+/* Session::block (:713-755), the attention step: rope_qknorm_f16 over the q and k heads
+ * of `fused` (weights qnorm/knorm, cos/sin) into q/k/v, the V transpose into vt, and
+ * f16 attention into attn_gu [tokens][hidden] with scale 1/sqrt(128). Query heads
+ * hidden/128, key-value heads kv/128, in a ratio of 1, 2 or 4; tokens >= 16. */
+int k2w8_block_attention(void *stream, const k2w8_block_cfg *cfg, int64_t index,
+                         const k2w8_block_weights *weights, const k2w8_block_buffers *buffers);
 /* Session::block (:756-839), after the attention (whose output the caller left in
  * attn_gu): prepare_gated_i8 over the gate half, gemm_wo + residual (gate = row 2),
  * prepare_norm_i8 (postnorm, rows 3/4), gemm_gu + SwiGLU into attn_gu,
@@ -388,7 +405,8 @@ int k2w8_block_post_attention(void *stream, const k2w8_block_cfg *cfg, int64_t i
 
 /* A recorded block loop (src/session/mod.rs:596-616): `layers` blocks, weights[i] for
  * block i, captured once from `stream` (a created stream) into a hipGraph over the
- * same buffers, replayed by k2w8_graph_launch. */
+ * same buffers, replayed by k2w8_graph_launch. Each block is pre_attention, the
+ * attention step when buffers->q is set, then post_attention. */
 typedef struct k2w8_graph k2w8_graph;
 int k2w8_blocks_record(void *stream, const k2w8_block_cfg *cfg, int64_t layers,
                        const k2w8_block_weights *weights, const k2w8_block_buffers *buffers,
@@ -398,7 +416,8 @@ void k2w8_graph_free(k2w8_graph *graph);
 
 /* The stage profile (src/session/mod.rs:449-479, 618-647): one eager pass over `layers`
  * blocks with events around every launch; stage_us[k] accumulates the microseconds of
- * stage k (labels from k2w8_block_stage_label) over all blocks. */
+ * stage k (labels from k2w8_block_stage_label) over all blocks, -1 for the attention
+ * stages when buffers->q is NULL. */
 int k2w8_blocks_profile(void *stream, const k2w8_block_cfg *cfg, int64_t layers,
                         const k2w8_block_weights *weights, const k2w8_block_buffers *buffers,
                         double *stage_us, int64_t stage_count);

@@ -4,11 +4,11 @@
 // (src/session/mod.rs:618-647, 449-479).
 //
 // Host code only: every launch goes through the library's own entry points, so the
-// argument checks and kernels are those of the single-kernel calls. The attention
-// stages between gemm_qkvg and prepare_gated (rope + q/k norm, V transpose, f16
-// attention) are outside this path: the caller runs them between
-// k2w8_block_pre_attention and k2w8_block_post_attention, leaving the attention output
-// in attn_gu.
+// argument checks and kernels are those of the single-kernel calls. The attention step
+// between gemm_qkvg and prepare_gated (q/k norm + rope, V transpose, f16 attention)
+// runs when the caller provides its workspaces (buffers->q set); otherwise the caller
+// runs its own attention between k2w8_block_pre_attention and
+// k2w8_block_post_attention, leaving the output in attn_gu.
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -114,7 +114,51 @@ int stage_down(void *s, const k2w8_block_cfg *c, int64_t i, const k2w8_block_wei
                                     b->x, mod_row(b, c, i, 5));
 }
 
+// The attention step (src/session/mod.rs:713-755). Heads: q_heads = hidden/128 at
+// column 0 of `fused`, kv_heads = (gate_offset - hidden)/256 of k at column hidden and
+// of v after them.
+struct Heads {
+  int64_t q, kv, group, capacity;
+};
+
+Heads heads_of(const k2w8_block_cfg *c) {
+  Heads h;
+  h.q = c->hidden / 128;
+  h.kv = (c->gate_offset - c->hidden) / 256;
+  h.group = h.kv > 0 ? h.q / h.kv : 0;
+  h.capacity = k2w8_shape_capacity(c->tokens);
+  return h;
+}
+
+int stage_rope(void *s, const k2w8_block_cfg *c, int64_t, const k2w8_block_weights *w,
+               const k2w8_block_buffers *b) {
+  const Heads h = heads_of(c);
+  const k2w8_rope_qknorm_cfg cfg = {c->qkvg, h.q, h.kv, c->hidden, c->eps};
+  return k2w8_rope_qknorm_f16(s, &cfg, c->tokens, b->fused, w->qnorm, w->knorm, b->cos, b->sin,
+                              b->q, b->k, b->v);
+}
+
+int stage_vt(void *s, const k2w8_block_cfg *c, int64_t, const k2w8_block_weights *,
+             const k2w8_block_buffers *b) {
+  const Heads h = heads_of(c);
+  const k2w8_v_transpose_cfg cfg = {h.kv * 128, h.capacity};
+  return k2w8_v_transpose(s, &cfg, c->tokens, b->v, b->vt);
+}
+
+int stage_attention(void *s, const k2w8_block_cfg *c, int64_t, const k2w8_block_weights *,
+                    const k2w8_block_buffers *b) {
+  const Heads h = heads_of(c);
+  // kernels/blocks.rs:94-103: q_stride = out_stride = hidden, kv_stride = kv width.
+  const k2w8_attention_cfg cfg = {c->hidden, h.kv * 128, c->hidden, c->tokens, h.capacity,
+                                  0.08838834764831845f};
+  return k2w8_attention_f16_grouped(s, &cfg, c->tokens, h.kv, h.group, b->q, b->k, b->vt,
+                                    b->attn_gu);
+}
+
 const Stage kPre[] = {{"prepare", stage_prepare}, {"gemm qkvg", stage_qkvg}};
+const Stage kAttn[] = {{"qk norm + rope", stage_rope},
+                       {"V transpose", stage_vt},
+                       {"f16 attention", stage_attention}};
 const Stage kPost[] = {{"prepare gated", stage_gated},
                        {"gemm wo + residual", stage_wo},
                        {"prepare", stage_post},
@@ -136,12 +180,65 @@ int check_call(const k2w8_block_cfg *c, int64_t index, const k2w8_block_weights 
                const k2w8_block_buffers *b, const char *stage) {
   int rc = check_cfg(c, stage);
   if (rc != K2W8_OK) return rc;
-  char msg[128];
+  char msg[256];
   if (!w || !b || !b->mods || index < 0) {
     snprintf(msg, sizeof msg, "%s: null weights, buffers or modulation table", stage);
     return k2w8_fail_invalid(msg);
   }
   return K2W8_OK;
+}
+
+bool with_attention(const k2w8_block_buffers *b) { return b && b->q; }
+
+int check_attention(const k2w8_block_cfg *c, const k2w8_block_weights *w,
+                    const k2w8_block_buffers *b, const char *stage) {
+  char msg[256];
+  const Heads h = heads_of(c);
+  if (c->hidden % 128 || (c->gate_offset - c->hidden) % 256 || h.kv < 1 ||
+      (h.group != 1 && h.group != 2 && h.group != 4) || h.group * h.kv != h.q) {
+    snprintf(msg, sizeof msg,
+             "%s: attention needs hidden/128 query heads and (gate_offset - hidden)/256 "
+             "key-value heads in a ratio of 1, 2 or 4",
+             stage);
+    return k2w8_fail_invalid(msg);
+  }
+  if (c->tokens < 16) {
+    snprintf(msg, sizeof msg, "%s: attention needs tokens >= 16", stage);
+    return k2w8_fail_invalid(msg);
+  }
+  if (!w->qnorm || !w->knorm || !b->q || !b->k || !b->v || !b->vt || !b->cos || !b->sin) {
+    snprintf(msg, sizeof msg, "%s: null qnorm/knorm or attention workspace", stage);
+    return k2w8_fail_invalid(msg);
+  }
+  return K2W8_OK;
+}
+
+int check_block(const k2w8_block_cfg *c, int64_t index, const k2w8_block_weights *w,
+                const k2w8_block_buffers *b, const char *stage) {
+  int rc = check_call(c, index, w, b, stage);
+  if (rc == K2W8_OK && with_attention(b)) rc = check_attention(c, w, b, stage);
+  return rc;
+}
+
+// One block: pre-attention stages, the attention step when its workspaces are given,
+// post-attention stages.
+int run_block(void *stream, const k2w8_block_cfg *c, int64_t index, const k2w8_block_weights *w,
+              const k2w8_block_buffers *b) {
+  int rc = run_stages(kPre, stream, c, index, w, b);
+  if (rc == K2W8_OK && with_attention(b)) rc = run_stages(kAttn, stream, c, index, w, b);
+  if (rc == K2W8_OK) rc = run_stages(kPost, stream, c, index, w, b);
+  return rc;
+}
+
+constexpr int64_t kPreCount = sizeof kPre / sizeof kPre[0];
+constexpr int64_t kAttnCount = sizeof kAttn / sizeof kAttn[0];
+constexpr int64_t kPostCount = sizeof kPost / sizeof kPost[0];
+constexpr int64_t kStageCount = kPreCount + kAttnCount + kPostCount;
+
+const Stage &stage_at(int64_t k) {
+  if (k < kPreCount) return kPre[k];
+  if (k < kPreCount + kAttnCount) return kAttn[k - kPreCount];
+  return kPost[k - kPreCount - kAttnCount];
 }
 
 }  // namespace
@@ -164,6 +261,16 @@ int k2w8_block_pre_attention(void *stream, const k2w8_block_cfg *cfg, int64_t in
   return run_stages(kPre, stream, cfg, index, weights, buffers);
 }
 
+int k2w8_block_attention(void *stream, const k2w8_block_cfg *cfg, int64_t index,
+                         const k2w8_block_weights *weights, const k2w8_block_buffers *buffers) {
+  const char *stage = "block_attention";
+  int rc = check_call(cfg, index, weights, buffers, stage);
+  if (rc != K2W8_OK) return rc;
+  if (!with_attention(buffers)) return k2w8_fail_invalid("block_attention: null q workspace");
+  if ((rc = check_attention(cfg, weights, buffers, stage)) != K2W8_OK) return rc;
+  return run_stages(kAttn, stream, cfg, index, weights, buffers);
+}
+
 int k2w8_block_post_attention(void *stream, const k2w8_block_cfg *cfg, int64_t index,
                               const k2w8_block_weights *weights, const k2w8_block_buffers *buffers) {
   int rc = check_call(cfg, index, weights, buffers, "block_post_attention");
@@ -179,7 +286,7 @@ int k2w8_blocks_record(void *stream, const k2w8_block_cfg *cfg, int64_t layers,
   *out = nullptr;
   if (layers < 1) return k2w8_fail_invalid("blocks_record: layers must be >= 1");
   for (int64_t i = 0; i < layers; ++i) {
-    int rc = check_call(cfg, i, weights + i, buffers, stage);
+    int rc = check_block(cfg, i, weights + i, buffers, stage);
     if (rc != K2W8_OK) return rc;
   }
   if (!stream)
@@ -190,10 +297,7 @@ int k2w8_blocks_record(void *stream, const k2w8_block_cfg *cfg, int64_t layers,
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
   if (e != hipSuccess) return k2w8_fail_runtime(stage, e);
-  for (int64_t i = 0; i < layers && rc == K2W8_OK; ++i) {
-    rc = run_stages(kPre, stream, cfg, i, weights + i, buffers);
-    if (rc == K2W8_OK) rc = run_stages(kPost, stream, cfg, i, weights + i, buffers);
-  }
+  for (int64_t i = 0; i < layers && rc == K2W8_OK; ++i) rc = run_block(stream, cfg, i, weights + i, buffers);
   auto g = std::make_unique<k2w8_graph>();
   e = hipStreamEndCapture(s, &g->graph);
   if (rc != K2W8_OK) return rc;
@@ -217,60 +321,53 @@ int k2w8_blocks_profile(void *stream, const k2w8_block_cfg *cfg, int64_t layers,
                         const k2w8_block_weights *weights, const k2w8_block_buffers *buffers,
                         double *stage_us, int64_t stage_count) {
   const char *stage = "blocks_profile";
-  const int64_t per_block = (int64_t)(sizeof kPre / sizeof kPre[0] + sizeof kPost / sizeof kPost[0]);
-  if (!stage_us || stage_count < per_block)
+  if (!stage_us || stage_count < kStageCount)
     return k2w8_fail_invalid("blocks_profile: stage_us must hold k2w8_block_stage_count() values");
   if (layers < 1) return k2w8_fail_invalid("blocks_profile: layers must be >= 1");
   for (int64_t i = 0; i < layers; ++i) {
-    int rc = check_call(cfg, i, weights + i, buffers, stage);
+    int rc = check_block(cfg, i, weights + i, buffers, stage);
     if (rc != K2W8_OK) return rc;
   }
+  const bool attention = with_attention(buffers);
+  std::vector<int64_t> order;  // the stages this pass runs, in order
+  for (int64_t k = 0; k < kStageCount; ++k) {
+    const bool is_attn = k >= kPreCount && k < kPreCount + kAttnCount;
+    stage_us[k] = is_attn && !attention ? -1.0 : 0.0;
+    if (!is_attn || attention) order.push_back(k);
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  for (int64_t k = 0; k < per_block; ++k) stage_us[k] = 0.0;
-  std::vector<hipEvent_t> ev((size_t)per_block * layers + 1);
+  std::vector<hipEvent_t> ev(order.size() * (size_t)layers + 1);
   for (auto &x : ev) {
     hipError_t e = hipEventCreate(&x);
     if (e != hipSuccess) return k2w8_fail_runtime(stage, e);
   }
-  auto destroy = [&] {
-    for (auto &x : ev) (void)hipEventDestroy(x);
-  };
   int rc = K2W8_OK;
   size_t at = 0;
   hipError_t e = hipEventRecord(ev[at++], s);
-  for (int64_t i = 0; i < layers && rc == K2W8_OK && e == hipSuccess; ++i) {
-    for (const Stage &st : kPre) {
-      if ((rc = st.run(stream, cfg, i, weights + i, buffers)) != K2W8_OK) break;
+  for (int64_t i = 0; i < layers && rc == K2W8_OK && e == hipSuccess; ++i)
+    for (int64_t k : order) {
+      if ((rc = stage_at(k).run(stream, cfg, i, weights + i, buffers)) != K2W8_OK) break;
       if ((e = hipEventRecord(ev[at++], s)) != hipSuccess) break;
     }
-    for (const Stage &st : kPost) {
-      if (rc != K2W8_OK || e != hipSuccess) break;
-      if ((rc = st.run(stream, cfg, i, weights + i, buffers)) != K2W8_OK) break;
-      if ((e = hipEventRecord(ev[at++], s)) != hipSuccess) break;
-    }
-  }
   if (rc == K2W8_OK && e == hipSuccess) e = hipEventSynchronize(ev[at - 1]);
   if (rc == K2W8_OK && e == hipSuccess) {
     for (size_t k = 1; k < at; ++k) {
       float ms = 0.0f;
       if ((e = hipEventElapsedTime(&ms, ev[k - 1], ev[k])) != hipSuccess) break;
-      stage_us[(k - 1) % per_block] += 1e3 * (double)ms;
+      stage_us[order[(k - 1) % order.size()]] += 1e3 * (double)ms;
     }
   }
-  destroy();
+  for (auto &x : ev) (void)hipEventDestroy(x);
   if (rc != K2W8_OK) return rc;
   if (e != hipSuccess) return k2w8_fail_runtime(stage, e);
   return k2w8_succeed();
 }
 
-int64_t k2w8_block_stage_count(void) {
-  return (int64_t)(sizeof kPre / sizeof kPre[0] + sizeof kPost / sizeof kPost[0]);
-}
+int64_t k2w8_block_stage_count(void) { return kStageCount; }
 
 const char *k2w8_block_stage_label(int64_t index) {
-  const int64_t pre = (int64_t)(sizeof kPre / sizeof kPre[0]);
-  if (index < 0 || index >= k2w8_block_stage_count()) return nullptr;
-  return index < pre ? kPre[index].label : kPost[index - pre].label;
+  if (index < 0 || index >= kStageCount) return nullptr;
+  return stage_at(index).label;
 }
 
 }  // extern "C"

@@ -103,11 +103,12 @@ class BlockCfg(ctypes.Structure):
 class BlockWeights(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in (
         "qkvg_q", "qkvg_s", "wo_q", "wo_s", "gu_q", "gu_s", "down_q", "down_s", "prenorm",
-        "postnorm")]
+        "postnorm", "qnorm", "knorm")]
 
 
 class BlockBuffers(ctypes.Structure):
-    _fields_ = [(n, ctypes.c_void_p) for n in ("x", "a_q", "a_s", "fused", "attn_gu", "mods")]
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "x", "a_q", "a_s", "fused", "attn_gu", "mods", "q", "k", "v", "vt", "cos", "sin")]
 
 
 class GemmCfg(ctypes.Structure):
@@ -170,6 +171,9 @@ SIGNATURES = {
     "k2w8_plan_span": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.POINTER(SpanInfo)]),
     "k2w8_plan_upload": (ctypes.c_int, [_P, _P, _P, _P, _I64]),
     "k2w8_block_pre_attention": (
+        ctypes.c_int, [_P, ctypes.POINTER(BlockCfg), _I64, ctypes.POINTER(BlockWeights),
+                       ctypes.POINTER(BlockBuffers)]),
+    "k2w8_block_attention": (
         ctypes.c_int, [_P, ctypes.POINTER(BlockCfg), _I64, ctypes.POINTER(BlockWeights),
                        ctypes.POINTER(BlockBuffers)]),
     "k2w8_block_post_attention": (

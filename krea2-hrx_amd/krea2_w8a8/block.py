@@ -20,10 +20,16 @@ def _p(t: torch.Tensor) -> int:
 class BlockSession:
     """``layers`` blocks at ``tokens`` rows. ``weights[i]`` holds block i's operands as
     device tensors: qkvg_q/qkvg_s, wo_q/wo_s, gu_q/gu_s, down_q/down_s (int8 rows at the
-    GEMM pitch, f32 scales) and the prenorm/postnorm f32 vectors."""
+    GEMM pitch, f32 scales), the prenorm/postnorm f32 vectors and, for the attention
+    step, the qnorm/knorm f32 [128] vectors.
+
+    With ``attention`` the session also owns the attention step's workspaces (q, k, v,
+    V^T with zero headroom; cos/sin, which the caller fills) and every block runs the
+    whole sequence of src/session/mod.rs:671-840; without it the caller runs its own
+    attention between ``pre_attention`` and ``post_attention``."""
 
     def __init__(self, weights, *, tokens, hidden, inter, qkvg, gate_offset, eps=1e-5,
-                 stream: torch.cuda.Stream | None = None):
+                 attention=False, stream: torch.cuda.Stream | None = None):
         self.layers = len(weights)
         self.cfg = BlockCfg(tokens, hidden, inter, qkvg, gate_offset, eps)
         self.stream = stream or torch.cuda.Stream()  # a created stream: graphs record from it
@@ -35,12 +41,24 @@ class BlockSession:
         self.fused = torch.zeros((tokens, qkvg), dtype=torch.float16, device=dev)
         self.attn_gu = torch.zeros(tokens * max(hidden, inter), dtype=torch.float16, device=dev)
         self.mods = torch.zeros((self.layers, 6, hidden), dtype=torch.float32, device=dev)
+        self.attention = attention
+        att = [0] * 6
+        if attention:
+            cap = int(lib().k2w8_shape_capacity(tokens))
+            kv = (gate_offset - hidden) // 2
+            self.q = torch.zeros((cap, hidden), dtype=torch.float16, device=dev)
+            self.k = torch.zeros((cap, kv), dtype=torch.float16, device=dev)
+            self.v = torch.zeros((cap, kv), dtype=torch.float16, device=dev)
+            self.vt = torch.zeros((kv, cap), dtype=torch.float16, device=dev)
+            self.cos = torch.ones((tokens, 128), dtype=torch.float32, device=dev)
+            self.sin = torch.zeros((tokens, 128), dtype=torch.float32, device=dev)
+            att = [_p(t) for t in (self.q, self.k, self.v, self.vt, self.cos, self.sin)]
         self._weights = weights  # keep the operands alive
         keys = [f for f, _ in BlockWeights._fields_]
         self._w = (BlockWeights * self.layers)(
-            *[BlockWeights(*[_p(w[k]) for k in keys]) for w in weights])
+            *[BlockWeights(*[_p(w[k]) if k in w else 0 for k in keys]) for w in weights])
         self._b = BlockBuffers(_p(self.x), _p(self.a_q), _p(self.a_s), _p(self.fused),
-                               _p(self.attn_gu), _p(self.mods))
+                               _p(self.attn_gu), _p(self.mods), *att)
         self._graph = ctypes.c_void_p()
 
     @staticmethod
@@ -57,6 +75,8 @@ class BlockSession:
                 "down_q": uploaded.operand(f"{p}.down"), "down_s": uploaded.scales(f"{p}.down"),
                 "prenorm": uploaded.vector(f"{p}.prenorm"),
                 "postnorm": uploaded.vector(f"{p}.postnorm"),
+                "qnorm": uploaded.vector(f"{p}.qnorm"),
+                "knorm": uploaded.vector(f"{p}.knorm"),
             })
         return BlockSession(weights, **shape)
 
@@ -67,15 +87,23 @@ class BlockSession:
         check(lib().k2w8_block_pre_attention(self._s(), ctypes.byref(self.cfg), index,
                                              ctypes.byref(self._w[index]), ctypes.byref(self._b)))
 
+    def attention_step(self, index: int) -> None:
+        """q/k norm + rope, V transpose and f16 attention into attn_gu (needs
+        ``attention``)."""
+        check(lib().k2w8_block_attention(self._s(), ctypes.byref(self.cfg), index,
+                                         ctypes.byref(self._w[index]), ctypes.byref(self._b)))
+
     def post_attention(self, index: int) -> None:
         check(lib().k2w8_block_post_attention(self._s(), ctypes.byref(self.cfg), index,
                                               ctypes.byref(self._w[index]), ctypes.byref(self._b)))
 
     def run(self) -> None:
-        """Every block eagerly on the session stream (attention left to the caller: the
-        post-attention stages read whatever attn_gu holds)."""
+        """Every block eagerly on the session stream. Without ``attention`` the
+        post-attention stages read whatever attn_gu holds."""
         for i in range(self.layers):
             self.pre_attention(i)
+            if self.attention:
+                self.attention_step(i)
             self.post_attention(i)
 
     def record(self) -> None:
@@ -99,6 +127,8 @@ class BlockSession:
                                         ctypes.byref(self._b), out, n))
         stages: dict = {}
         for k in range(n):
+            if out[k] < 0:  # a stage this session does not run
+                continue
             label = lib().k2w8_block_stage_label(k).decode()
             stages[label] = stages.get(label, 0.0) + out[k]
         return stages

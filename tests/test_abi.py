@@ -35,7 +35,7 @@ def test_every_declared_entry_point_is_exported_and_bound(k2):
     for name in names:
         assert hasattr(lib, name), name
         assert name in k2._lib.SIGNATURES, name
-    assert lib.k2w8_abi_version() == 1
+    assert lib.k2w8_abi_version() == 2
 
 
 def test_shape_rules_are_the_reference_rules(k2):
@@ -156,3 +156,79 @@ def test_quantized_forward_validates_before_any_launch(k2):
     # this case only checks the shape rejection of a zero-row call and a null cfg above
     assert lib.k2w8_quantized_forward(None, ctypes.byref(bad), 1 << 30, *args) == -1
     assert "2^30" in lib.k2w8_last_error().decode()
+
+
+def rope_call(k2, tokens=4, ptrs=None, **over):
+    cfg = dict(row_stride=15360, q_heads=48, kv_heads=12, k_offset=6144, eps=1e-5)
+    cfg.update(over)
+    c = k2._lib.RopeQknormCfg(**cfg)
+    return k2.lib().k2w8_rope_qknorm_f16(None, ctypes.byref(c), tokens, *(ptrs or [FAKE] * 8))
+
+
+@pytest.mark.parametrize("over,fragment", [
+    (dict(row_stride=15000), "row_stride"),
+    (dict(row_stride=0), "row_stride"),
+    (dict(q_heads=0), "q_heads"),
+    (dict(kv_heads=257), "kv_heads"),
+    (dict(k_offset=100), "k_offset"),
+    (dict(k_offset=14336), "fit row_stride"),
+    (dict(q_heads=121), "fit row_stride"),
+    (dict(eps=-1.0), "eps"),
+    (dict(tokens=0), "tokens"),
+    (dict(ptrs=[FAKE] * 7 + [None]), "null"),
+    (dict(ptrs=[ctypes.c_void_p(0x10008)] + [FAKE] * 7), "aligned"),
+])
+def test_rope_qknorm_rejects_what_the_reference_config_rejects(k2, over, fragment):
+    assert rope_call(k2, **over) == k2._lib.K2W8_INVALID_ARGUMENT
+    assert fragment in k2.lib().k2w8_last_error().decode()
+
+
+@pytest.mark.parametrize("width,capacity,rows,fragment", [
+    (1000, 4576, 10, "width"), (1536, 100, 10, "row_capacity"), (1536, 4576, 0, "rows"),
+    (1536, 4576, 4577, "rows")])
+def test_v_transpose_rejects_bad_shapes(k2, width, capacity, rows, fragment):
+    c = k2._lib.VTransposeCfg(width, capacity)
+    assert k2.lib().k2w8_v_transpose(None, ctypes.byref(c), rows, FAKE, FAKE) == -1
+    assert fragment in k2.lib().k2w8_last_error().decode()
+
+
+def attention_call(k2, token_count=4544, kv=12, group=4, **over):
+    cfg = dict(q_stride=6144, kv_stride=1536, out_stride=6144, tokens=4544, token_capacity=4576,
+               scale=0.088)
+    cfg.update(over)
+    c = k2._lib.AttentionCfg(**cfg)
+    return k2.lib().k2w8_attention_f16_grouped(None, ctypes.byref(c), token_count, kv, group,
+                                               FAKE, FAKE, FAKE, FAKE)
+
+
+@pytest.mark.parametrize("over,fragment", [
+    (dict(q_stride=6000), "strides"),
+    (dict(kv_stride=65536), "strides"),
+    (dict(tokens=15), "tokens"),
+    (dict(token_capacity=4544), "token_capacity"),
+    (dict(token_capacity=4570), "token_capacity"),
+    (dict(scale=0.0), "scale"),
+    (dict(token_count=0), "token_count"),
+    (dict(kv=13), "kv_head_count"),
+    (dict(kv=12, q_stride=4096), "kv_head_count"),
+    (dict(group=3), "group"),
+])
+def test_attention_rejects_what_the_reference_config_rejects(k2, over, fragment):
+    assert attention_call(k2, **over) == k2._lib.K2W8_INVALID_ARGUMENT
+    assert fragment in k2.lib().k2w8_last_error().decode()
+
+
+def test_block_attention_needs_its_workspaces_and_a_head_ratio(k2):
+    L = k2.lib()
+    cfg = k2._lib.BlockCfg(4544, 3072, 12288, 9216, 6144, 1e-5)
+    w = k2._lib.BlockWeights(*([0x10000] * 12))
+    b = k2._lib.BlockBuffers(*([0x10000] * 6 + [0] * 6))
+    assert L.k2w8_block_attention(None, ctypes.byref(cfg), 0, ctypes.byref(w), ctypes.byref(b)) == -1
+    assert "null q" in L.k2w8_last_error().decode()
+    b = k2._lib.BlockBuffers(*([0x10000] * 12))
+    bad = k2._lib.BlockCfg(4544, 3072, 12288, 9216, 3072 + 2 * 384, 1e-5)  # 24 q : 3 kv heads
+    assert L.k2w8_block_attention(None, ctypes.byref(bad), 0, ctypes.byref(w), ctypes.byref(b)) == -1
+    assert "ratio" in L.k2w8_last_error().decode()
+    short = k2._lib.BlockCfg(8, 3072, 12288, 9216, 6144, 1e-5)
+    assert L.k2w8_block_attention(None, ctypes.byref(short), 0, ctypes.byref(w), ctypes.byref(b)) == -1
+    assert "tokens" in L.k2w8_last_error().decode()
