@@ -30,6 +30,7 @@ sys.path.insert(0, os.path.join(ROOT, "krea2-hrx_amd"))
 
 PEAK_INT8_TOPS = 5000.0  # MI355X dense INT8 MFMA, 5.0 POP/s
 PEAK_HBM_GBS = 8000.0
+PEAK_F16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 COPY_PROBE_BYTES = 256 << 20
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_i8_qkv_4096x3072x9216_traffic.json")
 METRIC = "W8A8 GEMM TOPS and % of INT8 MFMA peak at M=4096,K=3072; DiT block linear ms"
@@ -53,7 +54,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
-              f"(--gpus {args.gpus} requested; the sharding design is in DESIGN.md)",
+              f"(--gpus {args.gpus} requested)",
               file=sys.stderr)
         sys.exit(2)
 
@@ -196,6 +197,11 @@ def main():
         result["config3_mlp_pair"] = mlp_pair(k2, torch, weights, hidden, args)
         torch.cuda.empty_cache()
         result["block_linears"] = block_linears(k2, torch, weights, hidden, args)
+        torch.cuda.empty_cache()
+        result["block_with_attention"] = block_linears(k2, torch, weights, hidden, args,
+                                                       attention=True)
+        torch.cuda.empty_cache()
+        result["attention_production"] = attention_production(k2, torch, args)
         torch.cuda.empty_cache()
         result["config5_skinny"] = skinny_sweep(k2, torch, weights, hidden, args)
         torch.cuda.empty_cache()
@@ -361,9 +367,13 @@ def skinny_sweep(k2, torch, weights, hidden, args):
     return rows
 
 
-def block_linears(k2, torch, weights, hidden, args):
+def block_linears(k2, torch, weights, hidden, args, attention=False):
     """the per-block linear sequence of a 3072-hidden DiT, M=4544, 8 blocks
     with the same weights, recorded once into a hipGraph and replayed.
+
+    With ``attention`` each block also runs the attention step between the QKV GEMM and
+    the gated prepare (q/k norm + rope, V transpose, f16 attention over 24 query and 12
+    key-value heads of 128, as the 9216-wide QKV output splits): the whole block.
 
     Per block, the reference's W8A8 stages in order (src/session/mod.rs:671-840, attention
     excluded): prepare_norm -> QKV [9216x3072]; prepare_gated(attn, gate) -> out-proj
@@ -382,13 +392,18 @@ def block_linears(k2, torch, weights, hidden, args):
     wd, sd = weights(H, pitch_i, 4103)
     norm = torch.rand(H, device="cuda") - 0.5
     block = {"qkvg_q": wq, "qkvg_s": sq, "wo_q": wo, "wo_s": so, "gu_q": wgu, "gu_s": sgu,
-             "down_q": wd, "down_s": sd, "prenorm": norm, "postnorm": norm}
+             "down_q": wd, "down_s": sd, "prenorm": norm, "postnorm": norm,
+             "qnorm": norm[:128].contiguous(), "knorm": norm[128:256].contiguous()}
     session = BlockSession([block] * blocks, tokens=M, hidden=H, inter=I, qkvg=9216,
-                           gate_offset=6144, eps=1e-6)
+                           gate_offset=6144, eps=1e-6, attention=attention)
     with torch.cuda.stream(session.stream):
         session.x.copy_(hidden(M, H, 4000).to(torch.bfloat16))
         session.attn_gu[: M * H].copy_(hidden(M, H, 4001).to(torch.float16).reshape(-1))
         session.mods[:, (2, 5)] = 1.0  # residual gates; scales and shifts zero
+        if attention:
+            ang = torch.rand((M, 64), device="cuda") * 6.3
+            session.cos.copy_(torch.cos(ang).repeat_interleave(2, dim=1))
+            session.sin.copy_(torch.sin(ang).repeat_interleave(2, dim=1))
     session.record()
     steps = max(2, args.steps // 8)
     for _ in range(max(1, args.warmup // 4)):
@@ -403,11 +418,59 @@ def block_linears(k2, torch, weights, hidden, args):
     ms_block = e0.elapsed_time(e1) / (steps * blocks)
     stages = {k: round(v / blocks, 1) for k, v in session.profile().items()}
     ops_block = 2.0 * M * H * (9216 + H + 2 * I) + 2.0 * M * I * H
-    return {"M": M, "hidden": H, "intermediate": I, "blocks": blocks, "replay": "hipGraph",
-            "ms_per_block": round(ms_block, 4),
-            "TOPS": round(ops_block / (ms_block * 1e-3) / 1e12, 1),
-            "ideal_ms_per_block_at_peak": round(ops_block / (PEAK_INT8_TOPS * 1e12) * 1e3, 4),
-            "stage_us_per_block_eager": stages}
+    out = {"M": M, "hidden": H, "intermediate": I, "blocks": blocks, "replay": "hipGraph",
+           "ms_per_block": round(ms_block, 4),
+           "TOPS": round(ops_block / (ms_block * 1e-3) / 1e12, 1),
+           "ideal_ms_per_block_at_peak": round(ops_block / (PEAK_INT8_TOPS * 1e12) * 1e3, 4),
+           "stage_us_per_block_eager": stages}
+    if attention:
+        flops_attn = 4.0 * M * M * 128 * (H // 128)
+        ideal = ops_block / (PEAK_INT8_TOPS * 1e12) + flops_attn / (PEAK_F16_TFLOPS * 1e12)
+        out.update({"attention": "24 query / 12 key-value heads of 128, non-causal, f16",
+                    "attention_flops_per_block": flops_attn,
+                    "attention_TFLOPs": round(flops_attn / (stages["f16 attention"] * 1e-6) / 1e12, 1),
+                    "ideal_ms_per_block_at_peak": round(ideal * 1e3, 4)})
+        del out["TOPS"]
+    return out
+
+
+def attention_production(k2, torch, args):
+    """The attention step at the reference's production heads (48 query, 12 key-value
+    heads of 128; src/session/mod.rs:37-45) for M=4544 tokens: rope_qknorm, V transpose
+    and the f16 attention kernel, each timed with HIP events (inputs resident)."""
+    M, QH, KVH = 4544, 48, 12
+    cap = k2.shape.capacity(M)
+    qkvg = (QH + 2 * KVH) * 128 + QH * 128
+    g = torch.Generator(device="cuda").manual_seed(4200)
+    fused = torch.randn((M, qkvg), device="cuda", generator=g).half()
+    qs = torch.rand(128, device="cuda", generator=g) - 0.5
+    ang = torch.rand((M, 64), device="cuda", generator=g) * 6.3
+    cos = torch.cos(ang).repeat_interleave(2, dim=1).contiguous()
+    sin = torch.sin(ang).repeat_interleave(2, dim=1).contiguous()
+    q = torch.zeros((cap, QH * 128), device="cuda", dtype=torch.float16)
+    k = torch.zeros((cap, KVH * 128), device="cuda", dtype=torch.float16)
+    v = torch.zeros_like(k)
+    vt = torch.zeros((KVH * 128, cap), device="cuda", dtype=torch.float16)
+    out = torch.empty((M, QH * 128), device="cuda", dtype=torch.float16)
+    rope = lambda _: k2.rope_qknorm_f16(fused, qs, qs, cos, sin, q, k, v, row_stride=qkvg,
+                                        q_heads=QH, kv_heads=KVH, k_offset=QH * 128, eps=1e-5)
+    trans = lambda _: k2.v_transpose(v, vt, width=KVH * 128, row_capacity=cap, rows=M)
+    attn = lambda _: k2.attention_f16(q, k, vt, out, q_stride=QH * 128, kv_stride=KVH * 128,
+                                      out_stride=QH * 128, tokens=M, token_capacity=cap,
+                                      scale=0.08838834764831845, kv_heads=KVH)
+    steps = max(3, args.steps // 5)
+    t_rope = event_timed(torch, rope, steps, 2)
+    t_trans = event_timed(torch, trans, steps, 2)
+    t_attn = event_timed(torch, attn, steps, 2)
+    flops = 4.0 * M * M * 128 * QH
+    rope_bytes = M * (QH + 2 * KVH) * 128 * 2 * 2 + 2 * M * 128 * 4
+    return {"M": M, "q_heads": QH, "kv_heads": KVH,
+            "rope_qknorm_us": round(t_rope * 1e6, 2),
+            "rope_qknorm_GBps": round(rope_bytes / t_rope / 1e9, 1),
+            "v_transpose_us": round(t_trans * 1e6, 2),
+            "attention_us": round(t_attn * 1e6, 2),
+            "attention_TFLOPs": round(flops / t_attn / 1e12, 1),
+            "attention_pct_of_f16_peak": round(100.0 * flops / t_attn / 1e12 / PEAK_F16_TFLOPS, 2)}
 
 
 def cpu_baseline(M, K, N, pitch, budget_s):
