@@ -44,6 +44,9 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="headline step only")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--probe", choices=["north_star", "skinny", "attention"],
+                   help="run one workload a few times and exit (a short program for "
+                        "rocprofv3 --pmc counter passes)")
     p.add_argument("--traffic-probe", action="store_true",
                    help="run a 256 MiB device copy and 5 QKV steps only (for rocprofv3 --pmc "
                         "FETCH_SIZE / WRITE_SIZE passes)")
@@ -85,6 +88,18 @@ def main():
         w = torch.randint(-127, 128, (rows, cols), generator=g, device=dev, dtype=torch.int8)
         s = torch.rand(rows, generator=g, device=dev) * 9e-3 + 1e-3
         return w, s
+
+    if args.probe:
+        args.steps, args.warmup = 3, 1
+        if args.probe == "north_star":
+            north_star(k2, torch, weights, hidden, args)
+        elif args.probe == "skinny":
+            skinny_sweep(k2, torch, weights, hidden, args, warm=False)
+        else:
+            attention_production(k2, torch, args)
+        torch.cuda.synchronize()
+        print(f"probe {args.probe} done", flush=True)
+        return
 
     # --- headline step: configs[1] -------------------------------------------------
     copies = 4  # 4 x ~140 MB of operands > 256 MB MALL
@@ -328,42 +343,60 @@ def mlp_pair(k2, torch, weights, hidden, args):
             "pct_of_int8_peak": round(100 * ops / sec / 1e12 / PEAK_INT8_TOPS, 2)}
 
 
-def skinny_sweep(k2, torch, weights, hidden, args):
+COLD_BYTES = 320 << 20  # weight copies rotated per call: more than the 256 MB MALL
+
+
+def skinny_sweep(k2, torch, weights, hidden, args, sizes=(1, 16, 77, 256, 512), warm=True):
     """text-encoder-shaped few-token regime, hidden 2560, intermediate 9728:
     QKV [4096 x 2560], SwiGLU up [2 x 9728 x 2560], down [2560 x 9728] (with residual) for
     M in {1, 16, 77, 256, 512}. HBM-bound on the weights at small M: reported as GB/s of
-    algorithmic bytes against the 8 TB/s peak."""
+    algorithmic bytes against the 8 TB/s peak.
+
+    ``GBps`` is MALL-cold: each call reads a different copy of the weights, enough copies
+    (more than 256 MB) that none is still in the MALL when it comes round again.
+    ``GBps_warm`` repeats one copy (weights served from the MALL)."""
     H, I = 2560, 9728
     pitch_i = k2.shape.gemm_pitch(I)
-    wq, sq = weights(4096, H, 5100)
-    wgu, sgu = weights(2 * I, H, 5101)
-    wd, sd = weights(H, pitch_i, 5102)
+
+    def copies(rows, cols, seed):
+        n = max(2, -(-COLD_BYTES // (rows * cols)))
+        return [weights(rows, cols, seed + 100 * c) for c in range(n)]
+
+    wq, wgu, wd = copies(4096, H, 5100), copies(2 * I, H, 5101), copies(H, pitch_i, 5102)
     one = torch.ones(H, device="cuda")
     rows = []
-    for M in (1, 16, 77, 256, 512):
+    for M in sizes:
         a_h = torch.randint(-127, 128, (M, H), device="cuda", dtype=torch.int8)
         a_i = torch.randint(-127, 128, (M, pitch_i), device="cuda", dtype=torch.int8)
         sc = torch.rand(M, device="cuda") * 1e-2 + 1e-3
         o_q = torch.empty((M, 4096), dtype=torch.float16, device="cuda")
         o_u = torch.empty((M, I), dtype=torch.float16, device="cuda")
         x = torch.zeros((M, H), dtype=torch.bfloat16, device="cuda")
+        cfg_q, cfg_u, cfg_d = k2.GemmConfig(H, 4096, H), k2.GemmConfig(H, 2 * I, H), \
+            k2.GemmConfig(I, H, pitch_i)
         cases = [
-            ("qkv", lambda _: k2.gemm_i8(a_h, wq, sq, sc, o_q, cfg=k2.GemmConfig(H, 4096, H)),
-             4096, H, 2 * M * 4096),
-            ("up_swiglu", lambda _: k2.gemm_i8_swiglu(a_h, wgu, sgu, sc, o_u,
-                                                      cfg=k2.GemmConfig(H, 2 * I, H)),
-             2 * I, H, 2 * M * I),
-            ("down_resid", lambda _: k2.gemm_i8_resid(a_i, wd, sd, sc, x, one,
-                                                      cfg=k2.GemmConfig(I, H, pitch_i)),
-             H, I, 4 * M * H),
+            ("qkv", lambda i, w: k2.gemm_i8(a_h, w[i % len(w)][0], w[i % len(w)][1], sc, o_q,
+                                            cfg=cfg_q), wq, 4096, H, 2 * M * 4096),
+            ("up_swiglu", lambda i, w: k2.gemm_i8_swiglu(a_h, w[i % len(w)][0], w[i % len(w)][1],
+                                                         sc, o_u, cfg=cfg_u),
+             wgu, 2 * I, H, 2 * M * I),
+            ("down_resid", lambda i, w: k2.gemm_i8_resid(a_i, w[i % len(w)][0], w[i % len(w)][1],
+                                                         sc, x, one, cfg=cfg_d),
+             wd, H, I, 4 * M * H),
         ]
-        for name, fn, n, k, out_bytes in cases:
-            sec = event_timed(torch, fn, max(20, args.steps), max(5, args.warmup))
+        for name, fn, w, n, k, out_bytes in cases:
             byts = n * k + M * k + 4 * n + 4 * M + out_bytes
-            rows.append({"M": M, "gemm": name, "N": n, "K": k, "us": round(sec * 1e6, 2),
-                         "GBps": round(byts / sec / 1e9, 1),
-                         "pct_of_hbm_peak": round(100 * byts / sec / 1e9 / PEAK_HBM_GBS, 1),
-                         "TOPS": round(2.0 * M * n * k / sec / 1e12, 1)})
+            steps = max(2 * len(w), args.steps)
+            sec = event_timed(torch, lambda i: fn(i, w), steps, len(w))
+            row = {"M": M, "gemm": name, "N": n, "K": k, "us": round(sec * 1e6, 2),
+                   "GBps": round(byts / sec / 1e9, 1),
+                   "pct_of_hbm_peak": round(100 * byts / sec / 1e9 / PEAK_HBM_GBS, 1),
+                   "TOPS": round(2.0 * M * n * k / sec / 1e12, 1)}
+            if warm:
+                sec_w = event_timed(torch, lambda i: fn(0, w), max(20, args.steps), 5)
+                row["us_warm"] = round(sec_w * 1e6, 2)
+                row["GBps_warm"] = round(byts / sec_w / 1e9, 1)
+            rows.append(row)
     return rows
 
 

@@ -356,7 +356,17 @@ inline GemmArgs args_of(const GemmLaunch &l, int epilogue) {
 #ifndef K2W8_MID_WM
 #define K2W8_MID_WM 4
 #endif
-constexpr int kBigWm = K2W8_BIG_WM, kBigWn = 8 / kBigWm;
+#ifndef K2W8_BIG_WAVES
+#define K2W8_BIG_WAVES 8
+#endif
+constexpr int kBigWm = K2W8_BIG_WM, kBigWn = K2W8_BIG_WAVES / kBigWm;
+#ifndef K2W8_BIG_BK
+#define K2W8_BIG_BK 128
+#endif
+#ifndef K2W8_BIG_STAGES
+#define K2W8_BIG_STAGES 2
+#endif
+constexpr int kBigBk = K2W8_BIG_BK, kBigStages = K2W8_BIG_STAGES;
 constexpr int kMidWm = K2W8_MID_WM, kMidWn = 8 / kMidWm;
 
 int device_cus() {
@@ -386,7 +396,7 @@ hipError_t launch_splitk_reduce(int epilogue, hipStream_t stream, const int32_t 
                                 int64_t stride, const gemm::GemmArgs &g);
 
 hipError_t configure_gemm_lds() {
-  hipError_t e = gemm::set_lds_tile<256, 256, kBigWm, kBigWn, 128, 2>();
+  hipError_t e = gemm::set_lds_tile<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>();
   if (e == hipSuccess) e = gemm::set_lds_tile<256, 128, kMidWm, kMidWn, 128, 2>();
   if (e == hipSuccess) e = gemm::set_lds_tile<128, 128, 2, 2, 128, 2>();
   if (e == hipSuccess) e = gemm::set_lds_tile<64, 64, 2, 2, 128, 2>();
@@ -433,7 +443,7 @@ hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &l) {
         ((l.m + 127) / 128) * ((l.n - n_big) / 128) <= kCus) {
       gemm::GemmArgs big = a, tail = a;
       big.n = (int)n_big;
-      hipError_t e = gemm::launch_tile<256, 256, kBigWm, kBigWn, 128, 2>(epilogue, stream, big);
+      hipError_t e = gemm::launch_tile<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>(epilogue, stream, big);
       if (e != hipSuccess) return e;
       tail.n = (int)(l.n - n_big);
       tail.w = a.w + n_big * l.lda;
@@ -446,11 +456,11 @@ hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &l) {
       return gemm::launch_tile<128, 128, 2, 2, 128, 2>(epilogue, stream, tail);
     }
 #endif
-    return gemm::launch_tile<256, 256, kBigWm, kBigWn, 128, 2>(epilogue, stream, a);
+    return gemm::launch_tile<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>(epilogue, stream, a);
   }
   // One round of 256x256 tiles over at least half the CUs beats two rounds of 256x128.
   if (l.n % 256 == 0 && tiles(256, 128) > kCus && 2 * tiles(256, 256) >= kCus)
-    return gemm::launch_tile<256, 256, kBigWm, kBigWn, 128, 2>(epilogue, stream, a);
+    return gemm::launch_tile<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>(epilogue, stream, a);
   if (tiles(256, 128) >= kCus)
     return gemm::launch_tile<256, 128, kMidWm, kMidWn, 128, 2>(epilogue, stream, a);
   if (tiles(128, 128) >= kCus) return gemm::launch_tile<128, 128, 2, 2, 128, 2>(epilogue, stream, a);
