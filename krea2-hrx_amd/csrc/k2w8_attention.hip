@@ -159,7 +159,9 @@ __global__ __launch_bounds__(256) void v_transpose_kernel(const uint16_t *x, uin
 //   V^T tile [128 ch][64 keys] f16, 128-byte rows in key order; chunk c of row r at
 //            c ^ ((r >> 1) & 7).
 // Two workgroups share a CU (LDS 64 KiB and at most 256 registers per lane each), so a
-// SIMD interleaves one wave's softmax with another's MFMAs.
+// SIMD interleaves one wave's softmax with another's MFMAs. The online softmax keeps a
+// per-query reference point m for exp2(s - m) that moves only when a score exceeds it
+// by more than kLag, so the accumulators are rarely rescaled.
 // ---------------------------------------------------------------------------------
 struct AttnArgs {
   const uint16_t *q, *k, *vt;
@@ -169,6 +171,7 @@ struct AttnArgs {
 };
 
 constexpr int kKeys = 64;
+constexpr float kLag = 8.0f;  // how far (log2 units) a score may exceed the exponent's reference point
 constexpr int kStage = 2 * 16384;
 
 __device__ __forceinline__ int key_of_row(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
@@ -329,7 +332,11 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
     }
     float m_tile = max3(max3(mx[0], mx[1], mx[2]), mx[3], mx[3]);
     m_tile = max3(m_tile, across_halves(m_tile, hf), m_tile) * c;
-    const float m_new = fmaxf(m_run, m_tile);
+    // The reference point of the exponent moves only when the tile's maximum exceeds
+    // it by more than kLag (base 2): weights stay below 2^kLag (f16 holds them at full
+    // relative precision), and the accumulators are rescaled far less often. Any
+    // reference point gives the same softmax after the final division.
+    const float m_new = m_tile > m_run + kLag ? m_tile : m_run;
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
     m_run = m_new;
     float part[4];
