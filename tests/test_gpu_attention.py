@@ -183,3 +183,51 @@ def test_attention_with_zero_queries_averages_v_at_production_size(tokens, q_hea
     mean = vt[:, :tokens].astype(np.float64).mean(axis=1).reshape(kv_heads, d)
     want = np.repeat(mean, 4, axis=0)  # query head h reads kv head h // 4
     assert np.all(np.abs(got - want[None]) <= 1e-5 + 2 ** -11 * np.abs(want[None]))
+
+
+def test_attention_at_the_minimum_capacity_and_with_wide_strides():
+    """capacity = tokens + 16 exactly (the last 64-key tile reaches past the buffers and is
+    clamped), strides wider than the heads in use (q 1024, kv 256, out 768 columns: the
+    reference kernel's strides are independent of the head count), one key-value head."""
+    tokens, cap, d = 96, 112, 128
+    q_stride, kv_stride, out_stride = 1024, 256, 768
+    rng = np.random.default_rng(96)
+    q = np.zeros((cap, q_stride), np.float16)
+    k = np.zeros((cap, kv_stride), np.float16)
+    v = np.zeros((cap, kv_stride), np.float16)
+    q[:tokens] = rng.standard_normal((tokens, q_stride))
+    k[:tokens] = rng.standard_normal((tokens, kv_stride))
+    v[:tokens] = rng.standard_normal((tokens, kv_stride))
+    vt = v.T.copy()
+    out = torch.full((tokens, out_stride), SENTINEL, dtype=torch.int16, device="cuda").view(
+        torch.float16)
+    k2.attention_f16(dev(q.view(np.uint16), torch.float16), dev(k.view(np.uint16), torch.float16),
+                     dev(vt.view(np.uint16), torch.float16), out, q_stride=q_stride,
+                     kv_stride=kv_stride, out_stride=out_stride, tokens=tokens,
+                     token_capacity=cap, scale=1 / np.sqrt(d), kv_heads=1)
+    sync()
+    got = host(out)
+    assert np.all(got[:, 512:] == SENTINEL)  # columns past the four heads untouched
+    ora = oracle.attention(q.view(np.uint16), k.view(np.uint16), vt.view(np.uint16),
+                           tokens=tokens, capacity=cap, q_stride=q_stride, kv_stride=kv_stride,
+                           out_stride=out_stride, kv_heads=1, scale=1 / np.sqrt(d), key_tile=64)
+    close(got[:, :512].view(np.float16), ora[:, :512].view(np.float16), 2e-3, 4e-3)
+
+
+def test_rope_qknorm_with_a_gap_before_k():
+    """k_offset past the q heads (a gap of unused columns) and eps = 0."""
+    tokens, qh, kvh, k_offset = 5, 2, 1, 512
+    stride = k_offset + 2 * kvh * 128 + 128
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((tokens, stride)).astype(np.float16)
+    bits = x.view(np.uint16)
+    qs = rng.uniform(-0.5, 0.5, 128).astype(np.float32)
+    ks = rng.uniform(-0.5, 0.5, 128).astype(np.float32)
+    ang = rng.uniform(0, 6.3, (tokens, 64)).astype(np.float32)
+    cos = np.repeat(np.cos(ang), 2, axis=1).astype(np.float32)
+    sin = np.repeat(np.sin(ang), 2, axis=1).astype(np.float32)
+    got = run_rope(bits, qs, ks, cos, sin, tokens, qh, kvh, stride, k_offset, eps=0.0)
+    want = oracle.rope_qknorm(bits, qs, ks, cos, sin, row_stride=stride, q_heads=qh,
+                              kv_heads=kvh, k_offset=k_offset, eps=0.0)
+    for g, w in zip(got, want):
+        assert np.array_equal(g, w)
