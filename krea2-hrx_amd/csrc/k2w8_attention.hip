@@ -223,17 +223,17 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
   // Transfers of one tile: wave w fills K rows 16w..16w+15 and V^T rows 32w..32w+31,
   // four 1 KiB instructions each; byte offsets from the tile's first key.
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
-  int k_row[4], v_key[4];
+  // Key row j of this lane's K transfers, the first key of its V^T transfers.
+  auto k_row_of = [&](int j) { return key_of_row(16 * wave + 4 * j + (lane >> 4)); };
+  auto v_key_of = [&](int j) { return ((lane & 7) ^ (((32 * wave + 8 * j + (lane >> 3)) >> 1) & 7)) * 8; };
   uint32_t k_off[4], v_off[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int r = 16 * wave + 4 * j + (lane >> 4);
-    k_row[j] = key_of_row(r);
     const int k_col = ((lane & 15) ^ (r & 15)) * 8;
-    k_off[j] = (uint32_t)(k_row[j] * a.kv_stride + k_col) * 2u;
+    k_off[j] = (uint32_t)(k_row_of(j) * a.kv_stride + k_col) * 2u;
     const int vr = 32 * wave + 8 * j + (lane >> 3);
-    v_key[j] = ((lane & 7) ^ ((vr >> 1) & 7)) * 8;
-    v_off[j] = (uint32_t)(vr * a.capacity + v_key[j]) * 2u;
+    v_off[j] = (uint32_t)(vr * a.capacity + v_key_of(j)) * 2u;
   }
   const uint16_t *k_head = a.k + kv_head * 128;
   const uint16_t *v_head = a.vt + (int64_t)kv_head * 128 * a.capacity;
@@ -250,13 +250,13 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
     } else {  // the last tile may reach past the buffers' rows: clamp (those keys are masked)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int key = min(key0 + k_row[j], a.capacity - 1) - key0;
-        dma16(so + (4 * wave + j) * 1024, kb, k_off[j] + (uint32_t)((key - k_row[j]) * a.kv_stride) * 2u);
+        const int key = min(key0 + k_row_of(j), a.capacity - 1) - key0;
+        dma16(so + (4 * wave + j) * 1024, kb, k_off[j] + (uint32_t)((key - k_row_of(j)) * a.kv_stride) * 2u);
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int first = min(key0 + v_key[j], a.capacity - 8) - key0;
-        dma16(so + 16384 + (4 * wave + j) * 1024, vb, v_off[j] + (uint32_t)(first - v_key[j]) * 2u);
+        const int first = min(key0 + v_key_of(j), a.capacity - 8) - key0;
+        dma16(so + 16384 + (4 * wave + j) * 1024, vb, v_off[j] + (uint32_t)(first - v_key_of(j)) * 2u);
       }
     }
   };
@@ -282,13 +282,13 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
   float m_run = -__builtin_inff(), l_run = 0.0f;
   const float c = a.scale_log2;
   // Per-lane LDS byte offsets within a stage of the K and V^T fragment rows.
-  int k_frag[8], v_frag[16];
+  // Rows kb*32 + col and cb*32 + col share the swizzle of row col: the blocks are
+  // constant offsets (8192 kb, 4096 cb) from the row-col addresses.
+  int k_frag[8], v_frag[4];
 #pragma unroll
-  for (int ks = 0; ks < 8; ++ks) k_frag[ks] = k_addr(col, 2 * ks + hf);  // row kb*32 + col: +8192*kb
+  for (int ks = 0; ks < 8; ++ks) k_frag[ks] = k_addr(col, 2 * ks + hf);
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) v_frag[cb * 4 + g] = v_addr(cb * 32 + col, 2 * g + hf);
+  for (int g = 0; g < 4; ++g) v_frag[g] = v_addr(col, 2 * g + hf);
 
   // One tile on a stage whose offset is a compile-time constant at each call.
   auto step = [&](int t, const int stage_off) __attribute__((always_inline)) {
@@ -368,7 +368,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
     for (int g = 0; g < 4; ++g)
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) {
-        const v8h vf = *reinterpret_cast<const v8h *>(stage + v_frag[cb * 4 + g]);
+        const v8h vf = *reinterpret_cast<const v8h *>(stage + cb * 4096 + v_frag[g]);
         o[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[g], o[cb], 0, 0, 0);
       }
   };
@@ -378,6 +378,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
     step(t, 0);
     if (t + 1 < tiles) step(t + 1, kStage);
   }
+
 
   // Row sums: each lane half holds the partial over its keys.
   const float inv = 1.0f / (l_run + across_halves(l_run, hf));
