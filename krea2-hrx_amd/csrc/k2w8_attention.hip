@@ -192,11 +192,11 @@ __device__ __forceinline__ void dma16(uint32_t lds, const void *base, uint32_t v
   asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(uniform_ptr(base)), "{m0}"(lds) : "memory");
 }
 
-__device__ __forceinline__ float max3(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
-}
+// Scores are never NaN, and this file is compiled with -fno-honor-nans: the maximum
+// selects v_max3_f32 without NaN-quieting copies of MFMA results. (An inline-asm
+// v_max3 would hide the MFMA result read from the compiler's hazard tracking, which
+// inserts the wait states a VALU read of an MFMA result needs.)
+__device__ __forceinline__ float max3(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
 
 // The value lane l ^ 32 holds. v_permlane32_swap exchanges lanes 32-63 of its first
 // operand with lanes 0-31 of its second: with x in both, the first result holds

@@ -231,3 +231,23 @@ def test_rope_qknorm_with_a_gap_before_k():
                               kv_heads=kvh, k_offset=k_offset, eps=0.0)
     for g, w in zip(got, want):
         assert np.array_equal(g, w)
+
+
+def test_attention_keeps_a_late_outlier_key_exact():
+    """Scores with a spread of about +-36 (q, k ~ N(0, 2.5^2)): some queries meet a key
+    far above every earlier one late in the sequence (the softmax maximum jumps by more
+    than 2^16 in weight). Every output must be finite and match the oracle."""
+    tokens, kv, group, d = 4544, 2, 4, 128
+    heads = group * kv
+    capacity = k2.shape.capacity(tokens)
+    rng = np.random.default_rng(6)
+    q, k, v = random_qkv(rng, tokens, capacity, heads, kv, 2.5)
+    vt = v.T.copy()
+    got = run_attention(q.view(np.uint16), k.view(np.uint16), vt.view(np.uint16), tokens=tokens,
+                        capacity=capacity, heads=heads, kv=kv, group=group)
+    assert np.all(np.isfinite(got.view(np.float16)))
+    ora = oracle.attention(q.view(np.uint16), k.view(np.uint16), vt.view(np.uint16),
+                           tokens=tokens, capacity=capacity, q_stride=heads * d, kv_stride=kv * d,
+                           out_stride=heads * d, kv_heads=kv, scale=1 / np.sqrt(d), group=group,
+                           key_tile=64)
+    close(got.view(np.float16), ora.view(np.float16), 2e-3, 4e-3)
