@@ -367,6 +367,9 @@ constexpr int kBigWm = K2W8_BIG_WM, kBigWn = K2W8_BIG_WAVES / kBigWm;
 #define K2W8_BIG_STAGES 2
 #endif
 constexpr int kBigBk = K2W8_BIG_BK, kBigStages = K2W8_BIG_STAGES;
+// A round of 128x128 tiles against a round of 256x256 ones (measured 27 us against
+// 61 us at K=3072), in units of tile width.
+constexpr int64_t kTailCost = 115;
 constexpr int kMidWm = K2W8_MID_WM, kMidWn = 8 / kMidWm;
 
 int device_cus() {
@@ -397,6 +400,7 @@ hipError_t launch_splitk_reduce(int epilogue, hipStream_t stream, const int32_t 
 
 hipError_t configure_gemm_lds() {
   hipError_t e = gemm::set_lds_tile<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>();
+  if (e == hipSuccess) e = gemm::set_lds_tile<256, 192, 4, 2, 128, 2>();
   if (e == hipSuccess) e = gemm::set_lds_tile<256, 128, kMidWm, kMidWn, 128, 2>();
   if (e == hipSuccess) e = gemm::set_lds_tile<128, 128, 2, 2, 128, 2>();
   if (e == hipSuccess) e = gemm::set_lds_tile<64, 64, 2, 2, 128, 2>();
@@ -424,43 +428,52 @@ int splitk_steps(const GemmLaunch &l, int64_t cus) {
 
 }  // namespace
 
-// Tile choice: the largest tile that still gives every CU a workgroup (for 256x256,
-// with a last partial round's columns re-tiled as one round of 128x128); when even
-// 64x64 tiles leave CUs idle, split K over 128x128 tiles; else the smallest tile.
+// Tile choice: 256x256 or 256x192 when they give at least a full round (or, for one
+// round, half the CUs), by rounds x width; else the largest of 256x128 and 128x128 that
+// gives every CU a workgroup; 64x64 for K up to 4096; split K over 128x128 tiles when
+// those cover at most half the CUs; else 64x64.
 hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &l) {
   if (l.m <= kSkinnyMaxTokens) return launch_skinny(epilogue, stream, l);
   gemm::GemmArgs a = gemm::args_of(l, epilogue);
   auto tiles = [&](int64_t bm, int64_t bn) { return ((l.m + bm - 1) / bm) * (l.n / bn); };
   const int64_t kCus = device_cus();
-  if (l.n % 256 == 0 && tiles(256, 256) >= kCus) {
-#ifndef K2W8_NO_TAIL_SPLIT
-    // Whole rounds of 256x256 tiles, then the columns of a last, mostly idle round as
-    // one round of 128x128 tiles (a quarter of the work each) when they fit in one.
+  // Wide tiles. A tile's time is about proportional to its width, so the candidates
+  // compare by rounds x width: 256x256 (whole rounds, the columns of a last, mostly
+  // idle round re-tiled as one round of 128x128 tiles, about 0.45 of a 256x256 round),
+  // or 256x192. Measured: QKV 4096x9216 144 -> 135 us, config 1 (4096x3072) 52 -> 46 us.
+  auto rounds = [&](int64_t t) { return (t + kCus - 1) / kCus; };
+  int64_t cost256 = INT64_MAX, n_big = 0;
+  if (l.n % 256 == 0 && (tiles(256, 256) >= kCus || (tiles(256, 128) > kCus && 2 * tiles(256, 256) >= kCus))) {
     const int64_t tm = (l.m + 255) / 256, total = tm * (l.n / 256);
-    const int64_t rest = total % kCus;
-    const int64_t n_big = (total / kCus) * kCus / tm * 256;
-    if (rest > 0 && rest * 2 <= kCus && n_big > 0 && n_big < l.n &&
-        ((l.m + 127) / 128) * ((l.n - n_big) / 128) <= kCus) {
-      gemm::GemmArgs big = a, tail = a;
-      big.n = (int)n_big;
-      hipError_t e = gemm::launch_tile<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>(epilogue, stream, big);
-      if (e != hipSuccess) return e;
-      tail.n = (int)(l.n - n_big);
-      tail.w = a.w + n_big * l.lda;
-      tail.w_scale = a.w_scale + n_big;
-      if (tail.gate) tail.gate = a.gate + n_big;
-      if (tail.bias) tail.bias = a.bias + n_big;
-      const int64_t out_col = epilogue == kEpiSwiglu ? n_big / 2 : n_big;
-      const int64_t elem = epilogue == kEpiAcc ? 4 : 2;
-      tail.c = static_cast<char *>(a.c) + out_col * elem;
-      return gemm::launch_tile<128, 128, 2, 2, 128, 2>(epilogue, stream, tail);
+    cost256 = rounds(total) * 256;
+#ifndef K2W8_NO_TAIL_SPLIT
+    const int64_t rest = total % kCus, nb = (total / kCus) * kCus / tm * 256;
+    if (total >= kCus && rest > 0 && rest * 2 <= kCus && nb > 0 && nb < l.n &&
+        ((l.m + 127) / 128) * ((l.n - nb) / 128) <= kCus) {
+      n_big = nb;
+      cost256 = (total / kCus) * 256 + kTailCost;
     }
 #endif
-    return gemm::launch_tile<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>(epilogue, stream, a);
   }
-  // One round of 256x256 tiles over at least half the CUs beats two rounds of 256x128.
-  if (l.n % 256 == 0 && tiles(256, 128) > kCus && 2 * tiles(256, 256) >= kCus)
-    return gemm::launch_tile<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>(epilogue, stream, a);
+  if (cost256 != INT64_MAX) {
+    // 256x192 tiles read 11% more LDS bytes per MFMA: they must win by 5%.
+    if (l.n % 192 == 0 && 2 * tiles(256, 192) >= kCus && rounds(tiles(256, 192)) * 192 * 21 < cost256 * 20)
+      return gemm::launch_tile<256, 192, 4, 2, 128, 2>(epilogue, stream, a);
+    if (n_big == 0) return gemm::launch_tile<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>(epilogue, stream, a);
+    gemm::GemmArgs big = a, tail = a;
+    big.n = (int)n_big;
+    hipError_t e = gemm::launch_tile<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>(epilogue, stream, big);
+    if (e != hipSuccess) return e;
+    tail.n = (int)(l.n - n_big);
+    tail.w = a.w + n_big * l.lda;
+    tail.w_scale = a.w_scale + n_big;
+    if (tail.gate) tail.gate = a.gate + n_big;
+    if (tail.bias) tail.bias = a.bias + n_big;
+    const int64_t out_col = epilogue == kEpiSwiglu ? n_big / 2 : n_big;
+    const int64_t elem = epilogue == kEpiAcc ? 4 : 2;
+    tail.c = static_cast<char *>(a.c) + out_col * elem;
+    return gemm::launch_tile<128, 128, 2, 2, 128, 2>(epilogue, stream, tail);
+  }
   if (tiles(256, 128) >= kCus)
     return gemm::launch_tile<256, 128, kMidWm, kMidWn, 128, 2>(epilogue, stream, a);
   if (tiles(128, 128) >= kCus) return gemm::launch_tile<128, 128, 2, 2, 128, 2>(epilogue, stream, a);

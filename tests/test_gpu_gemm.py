@@ -95,6 +95,11 @@ SHAPES = [
     (2000, 256, 9216, 64),
     # one round of 256x256 tiles where 256x128 would take two
     (300, 256, 19456, 0),
+    # 256x192 tiles where they take less time than 256x256 (rounds x width), including
+    # a SwiGLU output whose 32-row gate|up groups the 192-wide tiles keep whole
+    (4096, 256, 9216, 0),
+    (4096, 128, 3072, 64),
+    (2304, 128, 24576, 0),
     # split K over 128x128 tiles (fewer than half the CUs get a tile; or 64x64 tiles
     # would fill the chip but K is long)
     (320, 4224, 4096, 0),
