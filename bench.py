@@ -191,7 +191,7 @@ def main():
             "gemm_i8_TOPS": round(gemm_tops, 1),
         },
         "roofline": {
-            "kernel": "gemm_i8 (QKV, M=4096 K=3072 N=9216): 256x256 launch + 128x128 launch over the last 1024 columns",
+            "kernel": "gemm_i8 (QKV, M=4096 K=3072 N=9216): one launch of 256x192 tiles",
             "bound": "mfma",
             "achieved": round(gemm_tops, 1),
             "peak": PEAK_INT8_TOPS,
