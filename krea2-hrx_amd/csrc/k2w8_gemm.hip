@@ -25,6 +25,8 @@ namespace k2w8 {
 
 namespace gemm {
 
+typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));
+
 // Epilogue of one wave's (32 FM) x (32 FN) sub-tile at rows m_base.., columns n_base..
 template <int EPI, int FM, int FN>
 __device__ __forceinline__ void store_tile(const GemmArgs &g, v16i (&acc)[FM][FN], int m_base,
@@ -142,6 +144,120 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, v16i (&acc)[FM][FN
         }
         *reinterpret_cast<uint2 *>(out + 8 * q) = make_uint2(packed[0], packed[1]);
       }
+    }
+  }
+}
+
+// Epilogue through LDS, for the 16-bit outputs (plain, bias, residual, SwiGLU). The
+// f32 arithmetic up to the stored value's rounding runs on the accumulator layout,
+// as in store_tile; the packed 16-bit values then go to this wave's LDS region, one
+// 32-row block at a time, and come back as 16-byte runs of eight consecutive output
+// columns of one row, so every global store writes whole row segments (a store
+// instruction covers 64 x 16 bytes) instead of 32 rows x 16 bytes. The residual's
+// read-modify-write of x happens on that row layout, with the same f32 operations:
+// the staged value is bf16(v); x = bf16(x + bf16(gate * v)).
+// `region` holds 32 rows of kPitch bytes (the output columns plus 16 bytes, which
+// spreads the rows' 8-byte writes over the banks).
+template <int EPI, int FM, int FN>
+__device__ __forceinline__ void store_tile_lds(const GemmArgs &g, v16i (&acc)[FM][FN], int m_base,
+                                               int n_base, int fr, int kh, int lane,
+                                               uint8_t *region) {
+  constexpr int kCols = EPI == kEpiSwiglu ? 16 * FN : 32 * FN;  // output columns
+  constexpr int kPitch = kCols * 2 + 16;
+  constexpr int kChunks = kCols / 8;  // 16-byte runs per row
+  constexpr int kReads = (32 * kChunks + 63) / 64;
+  const int out_base = EPI == kEpiSwiglu ? n_base / 2 : n_base;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int m = m_base + i * 32 + fr;
+    const float as = g.a_scale[m < g.m ? m : g.m - 1];
+    uint8_t *row = region + fr * kPitch;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      // Per-channel vectors of this lane's channels: n = n_base + 32j + 8q + 4kh + r
+      // (SwiGLU: registers 8-15 are the up channels, 16 further on).
+      float ws[16], extra[16];
+      const int nb = n_base + j * 32 + kh * 4;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int ch = (EPI == kEpiSwiglu && q >= 2) ? nb + 16 + 8 * (q - 2) : nb + 8 * q;
+        const float4 v = *reinterpret_cast<const float4 *>(g.w_scale + ch);
+        ws[4 * q] = v.x; ws[4 * q + 1] = v.y; ws[4 * q + 2] = v.z; ws[4 * q + 3] = v.w;
+        if (EPI == kEpiBias) {
+          const uint2 b = *reinterpret_cast<const uint2 *>(g.bias + ch);
+          extra[4 * q] = f16_value(b.x & 0xffffu); extra[4 * q + 1] = f16_value(b.x >> 16);
+          extra[4 * q + 2] = f16_value(b.y & 0xffffu); extra[4 * q + 3] = f16_value(b.y >> 16);
+        }
+      }
+      if (EPI == kEpiSwiglu) {
+        // registers 0-7: gate channels 8q+4kh+r (q<2), 8-15: the matching ups
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          uint32_t packed[2];
+#pragma unroll
+          for (int r = 0; r < 4; r += 2) {
+            float g0 = ((float)acc[i][j][4 * q + r] * ws[4 * q + r]) * as;
+            float g1 = ((float)acc[i][j][4 * q + r + 1] * ws[4 * q + r + 1]) * as;
+            float u0 = ((float)acc[i][j][8 + 4 * q + r] * ws[8 + 4 * q + r]) * as;
+            float u1 = ((float)acc[i][j][8 + 4 * q + r + 1] * ws[8 + 4 * q + r + 1]) * as;
+            bf16_round2(g0, g1);
+            bf16_round2(u0, u1);
+            float s0 = g0 * sigmoid(g0), s1 = g1 * sigmoid(g1);
+            bf16_round2(s0, s1);
+            float p0 = s0 * u0, p1 = s1 * u1;
+            bf16_round2(p0, p1);
+            packed[r >> 1] = f16_pack2(p0, p1);
+          }
+          *reinterpret_cast<uint2 *>(row + 2 * (j * 16 + 8 * q + 4 * kh)) = make_uint2(packed[0], packed[1]);
+        }
+        continue;
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint32_t packed[2];
+#pragma unroll
+        for (int r = 0; r < 4; r += 2) {
+          const int e = 4 * q + r;
+          float v0 = ((float)acc[i][j][e] * ws[e]) * as;
+          float v1 = ((float)acc[i][j][e + 1] * ws[e + 1]) * as;
+          if (EPI == kEpiBias) {
+            v0 = v0 + extra[e];
+            v1 = v1 + extra[e + 1];
+          }
+          if (EPI == kEpiResid) {
+            packed[r >> 1] = bf16_pack2(v0, v1);
+          } else {
+            bf16_round2(v0, v1);
+            packed[r >> 1] = f16_pack2(v0, v1);
+          }
+        }
+        *reinterpret_cast<uint2 *>(row + 2 * (j * 32 + 8 * q + 4 * kh)) = make_uint2(packed[0], packed[1]);
+      }
+    }
+    // This wave's own LDS writes, read back in row order (LDS serves one wave in order).
+#pragma unroll
+    for (int s = 0; s < kReads; ++s) {
+      const int idx = s * 64 + lane;
+      const int r = idx / kChunks, c = idx - r * kChunks;
+      const int tok = m_base + i * 32 + r;
+      if (r >= 32 || tok >= g.m) continue;
+      v4u_t v = *reinterpret_cast<const v4u_t *>(region + r * kPitch + 16 * c);
+      uint16_t *out = static_cast<uint16_t *>(g.c) + (int64_t)tok * g.ldc + out_base + 8 * c;
+      if (EPI == kEpiResid) {
+        const v4u_t prior = *reinterpret_cast<const v4u_t *>(out);
+        const float4 g0 = *reinterpret_cast<const float4 *>(g.gate + n_base + 8 * c);
+        const float4 g1 = *reinterpret_cast<const float4 *>(g.gate + n_base + 8 * c + 4);
+        const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          float a0 = __uint_as_float(v[w] << 16) * gv[2 * w];
+          float a1 = __uint_as_float(v[w] & 0xffff0000u) * gv[2 * w + 1];
+          bf16_round2(a0, a1);
+          v[w] = bf16_pack2(__uint_as_float(prior[w] << 16) + a0,
+                            __uint_as_float(prior[w] & 0xffff0000u) + a1);
+        }
+      }
+      *reinterpret_cast<v4u_t *>(out) = v;
     }
   }
 }
@@ -277,7 +393,16 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
     }
   }
 
-  store_tile<EPI, FM, FN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, fr, kh);
+  if constexpr (EPI == kEpiAcc) {
+    store_tile<EPI, FM, FN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, fr, kh);
+  } else {
+    // Every wave has finished reading the stages: reuse the LDS for the epilogue.
+    constexpr int kRegion = 32 * ((EPI == kEpiSwiglu ? 16 * FN : 32 * FN) * 2 + 16);
+    static_assert(kRegion * kWaves <= STAGES * kStage, "epilogue staging fits the stages");
+    __syncthreads();
+    store_tile_lds<EPI, FM, FN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, fr, kh, lane,
+                                smem + wave * kRegion);
+  }
 }
 
 template <int BM, int BN, int WM, int WN, int BK, int STAGES>
