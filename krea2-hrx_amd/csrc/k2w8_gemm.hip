@@ -148,7 +148,8 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, v16i (&acc)[FM][FN
   }
 }
 
-// Epilogue through LDS, for the 16-bit outputs (plain, bias, residual, SwiGLU). The
+// Epilogue through LDS (every output but split-K's int32 slices, which also go through
+// it: 4-byte elements). The
 // f32 arithmetic up to the stored value's rounding runs on the accumulator layout,
 // as in store_tile; the packed 16-bit values then go to this wave's LDS region, one
 // 32-row block at a time, and come back as 16-byte runs of eight consecutive output
@@ -163,23 +164,31 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs &g, v16i (&acc)[FM
                                                int n_base, int fr, int kh, int lane,
                                                uint8_t *region) {
   constexpr int kCols = EPI == kEpiSwiglu ? 16 * FN : 32 * FN;  // output columns
-  constexpr int kPitch = kCols * 2 + 16;
-  constexpr int kChunks = kCols / 8;  // 16-byte runs per row
+  constexpr int kElem = EPI == kEpiAcc ? 4 : 2;                  // output bytes
+  constexpr int kPitch = kCols * kElem + 16;
+  constexpr int kChunks = kCols * kElem / 16;  // 16-byte runs per row
   constexpr int kReads = (32 * kChunks + 63) / 64;
   const int out_base = EPI == kEpiSwiglu ? n_base / 2 : n_base;
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int m = m_base + i * 32 + fr;
-    const float as = g.a_scale[m < g.m ? m : g.m - 1];
+    const float as = EPI == kEpiAcc ? 1.0f : g.a_scale[m < g.m ? m : g.m - 1];
     uint8_t *row = region + fr * kPitch;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
+      if (EPI == kEpiAcc) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<v4i *>(row + 4 * (j * 32 + 8 * q + 4 * kh)) =
+              v4i{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        continue;
+      }
       // Per-channel vectors of this lane's channels: n = n_base + 32j + 8q + 4kh + r
       // (SwiGLU: registers 8-15 are the up channels, 16 further on).
       float ws[16], extra[16];
       const int nb = n_base + j * 32 + kh * 4;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < 4 && EPI != kEpiAcc; ++q) {
         const int ch = (EPI == kEpiSwiglu && q >= 2) ? nb + 16 + 8 * (q - 2) : nb + 8 * q;
         const float4 v = *reinterpret_cast<const float4 *>(g.w_scale + ch);
         ws[4 * q] = v.x; ws[4 * q + 1] = v.y; ws[4 * q + 2] = v.z; ws[4 * q + 3] = v.w;
@@ -242,6 +251,12 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs &g, v16i (&acc)[FM
       const int tok = m_base + i * 32 + r;
       if (r >= 32 || tok >= g.m) continue;
       v4u_t v = *reinterpret_cast<const v4u_t *>(region + r * kPitch + 16 * c);
+      if (EPI == kEpiAcc) {
+        int32_t *out = static_cast<int32_t *>(g.c) + (int64_t)blockIdx.y * g.split_stride +
+                       (int64_t)tok * g.ldc + n_base + 4 * c;
+        *reinterpret_cast<v4u_t *>(out) = v;
+        continue;
+      }
       uint16_t *out = static_cast<uint16_t *>(g.c) + (int64_t)tok * g.ldc + out_base + 8 * c;
       if (EPI == kEpiResid) {
         const v4u_t prior = *reinterpret_cast<const v4u_t *>(out);
@@ -393,15 +408,15 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
     }
   }
 
-  if constexpr (EPI == kEpiAcc) {
-    store_tile<EPI, FM, FN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, fr, kh);
-  } else {
-    // Every wave has finished reading the stages: reuse the LDS for the epilogue.
-    constexpr int kRegion = 32 * ((EPI == kEpiSwiglu ? 16 * FN : 32 * FN) * 2 + 16);
-    static_assert(kRegion * kWaves <= STAGES * kStage, "epilogue staging fits the stages");
+  // Every wave has finished reading the stages: reuse the LDS for the epilogue.
+  constexpr int kRegion =
+      32 * ((EPI == kEpiSwiglu ? 16 * FN : 32 * FN) * (EPI == kEpiAcc ? 4 : 2) + 16);
+  if constexpr (kRegion * kWaves <= STAGES * kStage) {
     __syncthreads();
     store_tile_lds<EPI, FM, FN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, fr, kh, lane,
                                 smem + wave * kRegion);
+  } else {  // int32 output of the 256x256 tile: 135 KiB would not fit; direct stores
+    store_tile<EPI, FM, FN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, fr, kh);
   }
 }
 
