@@ -509,7 +509,14 @@ constexpr int kBigWm = K2W8_BIG_WM, kBigWn = K2W8_BIG_WAVES / kBigWm;
 constexpr int kBigBk = K2W8_BIG_BK, kBigStages = K2W8_BIG_STAGES;
 // A round of 128x128 tiles against a round of 256x256 ones (measured 27 us against
 // 61 us at K=3072), in units of tile width.
-constexpr int64_t kTailCost = 115;
+#ifndef K2W8_TAIL_COST
+#define K2W8_TAIL_COST 115
+#endif
+constexpr int64_t kTailCost = K2W8_TAIL_COST;
+#ifndef K2W8_USE_192
+#define K2W8_USE_192 1
+#endif
+constexpr bool kUse192 = K2W8_USE_192;
 constexpr int kMidWm = K2W8_MID_WM, kMidWn = 8 / kMidWm;
 
 int device_cus() {
@@ -597,7 +604,8 @@ hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &l) {
   }
   if (cost256 != INT64_MAX) {
     // 256x192 tiles read 11% more LDS bytes per MFMA: they must win by 5%.
-    if (l.n % 192 == 0 && 2 * tiles(256, 192) >= kCus && rounds(tiles(256, 192)) * 192 * 21 < cost256 * 20)
+    if (kUse192 && l.n % 192 == 0 && 2 * tiles(256, 192) >= kCus &&
+        rounds(tiles(256, 192)) * 192 * 21 < cost256 * 20)
       return gemm::launch_tile<256, 192, 4, 2, 128, 2>(epilogue, stream, a);
     if (n_big == 0) return gemm::launch_tile<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>(epilogue, stream, a);
     gemm::GemmArgs big = a, tail = a;
