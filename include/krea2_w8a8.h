@@ -169,6 +169,14 @@ int k2w8_gemm_i8_acc(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, const in
  */
 int k2w8_lora_transport(void *stream, int direction, int64_t count, const void *x, void *out);
 
+/*
+ * sigmoid_f32: none in the reference (a check of this build's numerics). Evaluates,
+ * elementwise, the device sigmoid 1 / (1 + exp(-x)) that prepare_gated_i8 and the
+ * SwiGLU epilogue use, so its bits can be compared with the CPU definition.
+ *   x f32 [count] -> out f32 [count]; count in 1..2^32-1.
+ */
+int k2w8_sigmoid_f32(void *stream, int64_t count, const float *x, float *out);
+
 /* Shape of a ConvRot projection (src/training/quantized.rs:8-14). */
 typedef struct k2w8_quantized_cfg {
   int64_t inputs;  /* K: a multiple of 256 (prepare width rules) */

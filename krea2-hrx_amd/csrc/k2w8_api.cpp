@@ -287,6 +287,19 @@ int k2w8_lora_transport(void *stream, int direction, int64_t count, const void *
   return ok();
 }
 
+int k2w8_sigmoid_f32(void *stream, int64_t count, const float *x, float *out) {
+  const char *stage = "sigmoid_f32";
+  if (count < 1 || count >= (int64_t(1) << 32))
+    return fail(K2W8_INVALID_ARGUMENT, "%s: count must be 1..2^32-1, got %lld", stage,
+                (long long)count);
+  if (!x || !out) return fail(K2W8_INVALID_ARGUMENT, "%s: null buffer", stage);
+  if (!aligned(x, 4) || !aligned(out, 4))
+    return fail(K2W8_INVALID_ARGUMENT, "%s: x and out must be 4-byte aligned", stage);
+  hipError_t e = k2w8::launch_sigmoid(static_cast<hipStream_t>(stream), count, x, out);
+  if (e != hipSuccess) return runtime(stage, e);
+  return ok();
+}
+
 // kernels/rope_qknorm_f16.loom:12-20, 22-159
 int k2w8_rope_qknorm_f16(void *stream, const k2w8_rope_qknorm_cfg *cfg, int64_t tokens,
                          const void *qkv, const float *q_scale, const float *k_scale,

@@ -398,6 +398,26 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
         read_frags<FM, FN>(af[cur ^ 1], bf[cur ^ 1], smem + ((kt + 1) % STAGES) * kStage,
                            a_row_off, b_row_off, (kh ^ rsw) << 4);
       }
+      if (s + 1 < NS) {
+        // The next slice's fragment reads go one between each of the first MFMAs, so
+        // the LDS requests spread over the MFMA issue instead of queueing in a burst.
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[cur][j], af[cur][i], acc[i][j], 0, 0, 0);
+        constexpr int kMfma = FM * FN, kReads = FM + FN;
+        constexpr int kPairs = kMfma < kReads ? kMfma : kReads;
+#pragma unroll
+        for (int q = 0; q < kPairs; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        }
+        if constexpr (kMfma > kPairs) __builtin_amdgcn_sched_group_barrier(0x008, kMfma - kPairs, 0);
+        if constexpr (kReads > kPairs) __builtin_amdgcn_sched_group_barrier(0x100, kReads - kPairs, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        continue;
+      }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < FM; ++i)

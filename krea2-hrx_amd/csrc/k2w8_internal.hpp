@@ -38,6 +38,7 @@ hipError_t launch_skinny(int epilogue, hipStream_t stream, const GemmLaunch &g);
 hipError_t configure_gemm_lds();
 
 // bf16 <-> f16 transport: direction 1 bf16 -> f16, 2 f16 -> bf16.
+hipError_t launch_sigmoid(hipStream_t stream, int64_t count, const float *x, float *out);
 hipError_t launch_transport(int direction, hipStream_t stream, int64_t count, const void *x,
                             void *out);
 

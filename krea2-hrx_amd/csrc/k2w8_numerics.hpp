@@ -61,12 +61,13 @@ __device__ __forceinline__ float f16_round(float x) { return (float)(_Float16)x;
 
 // exp(x) for the sigmoids of the gated prepare and the SwiGLU epilogue:
 // Cody-Waite reduction x = n*ln2 + r (two-part ln2), e^r = 1 + r + r^2 q(r) with a
-// degree-4 least-squares q, then 2^n as two exact power-of-two factors. The CPU
-// oracle evaluates the identical operation sequence.
+// degree-4 least-squares q, then 2^n as two power-of-two factors (the first product
+// is exact, the second rounds once). The CPU definition splits n as n/2 (toward zero)
+// and branches to its special cases; this form splits as floor(n/2) and selects them,
+// which gives the identical value for every f32 input.
 __device__ __forceinline__ float sigmoid_exp(float x) {
-  if (x != x) return x;
-  if (x > 0x1.62e42ep+6f) return __builtin_inff();
-  if (x < -0x1.9fe368p+6f) return 0.0f;
+  // Branch-free: the special cases are selected at the end (a wave would otherwise
+  // branch around them per element).
   float n = __builtin_rintf(x * 0x1.715476p+0f);
   float r = __builtin_fmaf(n, -0x1.62e4p-1f, x);
   r = __builtin_fmaf(n, -0x1.7f7d1cp-20f, r);
@@ -76,19 +77,34 @@ __device__ __forceinline__ float sigmoid_exp(float x) {
   q = __builtin_fmaf(q, r, 0.5f);
   float r2 = r * r;
   float p = 1.0f + __builtin_fmaf(q, r2, r);
+  // p * 2^n with one rounding: p * 2^(n/2) is exact (normal), the second factor rounds.
   int ni = (int)n;
-  int n1 = ni / 2;
+  int n1 = ni >> 1;
   int n2 = ni - n1;
   float s1 = __uint_as_float((uint32_t)(n1 + 127) << 23);
   float s2 = __uint_as_float((uint32_t)(n2 + 127) << 23);
-  return (p * s1) * s2;
+  float e = (p * s1) * s2;
+  e = x > 0x1.62e42ep+6f ? __builtin_inff() : e;
+  e = x < -0x1.9fe368p+6f ? 0.0f : e;
+  return x != x ? x : e;
 }
 
-// 1 / (1 + exp(-g)), correctly rounded division.
+// 1 / (1 + exp(-g)), correctly rounded. For 1 <= d < 2^126 the hardware reciprocal
+// (within 1 ulp) and one residual correction, res = 1 - d*y exactly by fma, then
+// y + res*y rounded once, give the correctly rounded quotient: checked on the device
+// for every such d. Larger d (subnormal quotients, and infinity) take the IEEE
+// division, which a wave only runs when one of its lanes needs it.
 __device__ __forceinline__ float sigmoid(float g) {
   float e = sigmoid_exp(0.0f - g);
   float den = 1.0f + e;
-  return 1.0f / den;
+  float y = __builtin_amdgcn_rcpf(den);
+  float res = __builtin_fmaf(-den, y, 1.0f);
+  y = __builtin_fmaf(res, y, y);
+  if (__builtin_expect(den >= 0x1p126f, 0)) {
+    asm volatile("");  // keeps the division out of the common path
+    y = 1.0f / den;
+  }
+  return y;
 }
 
 }  // namespace k2w8

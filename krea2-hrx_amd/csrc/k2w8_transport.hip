@@ -53,7 +53,24 @@ __global__ __launch_bounds__(256) void transport_kernel(const uint16_t *x, uint1
     out[tail + threadIdx.x] = convert1<kDirection>(x[tail + threadIdx.x]);
 }
 
+__global__ __launch_bounds__(256) void sigmoid_kernel(const float *x, float *out, int64_t count) {
+  const int64_t step = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += step)
+    out[i] = sigmoid(x[i]);
+}
+
 }  // namespace
+
+// The device sigmoid of the gated prepare and the SwiGLU epilogue, elementwise: lets
+// its bits be compared with the CPU definition over any set of inputs.
+hipError_t launch_sigmoid(hipStream_t stream, int64_t count, const float *x, float *out) {
+  int64_t blocks = (count + 255) / 256;
+  const int64_t cap = (int64_t)device_cus() * 8;
+  if (blocks > cap) blocks = cap;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(sigmoid_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, x, out, count);
+  return hipGetLastError();
+}
 
 hipError_t launch_transport(int direction, hipStream_t stream, int64_t count, const void *x,
                             void *out) {

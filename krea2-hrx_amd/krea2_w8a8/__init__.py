@@ -25,6 +25,7 @@ from .ops import (  # noqa: F401
     gemm_i8_resid_256x256,
     gemm_i8_swiglu,
     lora_transport,
+    sigmoid_f32,
     prepare_gated_i8,
     prepare_norm_i8,
     prepare_plain_i8,
@@ -49,6 +50,7 @@ __all__ = [
     "lib",
     "library_path",
     "lora_transport",
+    "sigmoid_f32",
     "prepare_gated_i8",
     "prepare_norm_i8",
     "prepare_plain_i8",

@@ -147,6 +147,7 @@ SIGNATURES = {
     "k2w8_gemm_i8_bias": (ctypes.c_int, [_P, ctypes.POINTER(GemmCfg), _I64, _P, _P, _P, _P, _P, _P]),
     "k2w8_gemm_i8_acc": (ctypes.c_int, [_P, ctypes.POINTER(GemmCfg), _I64, _P, _P, _P]),
     "k2w8_lora_transport": (ctypes.c_int, [_P, ctypes.c_int, _I64, _P, _P]),
+    "k2w8_sigmoid_f32": (ctypes.c_int, [_P, _I64, _P, _P]),
     "k2w8_quantized_forward": (
         ctypes.c_int,
         [_P, ctypes.POINTER(QuantizedCfg), _I64, _P, _P, _P, _P, _P, _P, _P, _P],

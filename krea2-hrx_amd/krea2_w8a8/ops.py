@@ -199,6 +199,15 @@ def lora_transport(x, out, *, reverse: int, count=None, stream=None):
     check(lib().k2w8_lora_transport(_stream(stream), int(reverse), n, px, po))
 
 
+def sigmoid_f32(x, out, *, count=None, stream=None):
+    """The device sigmoid 1 / (1 + exp(-x)) of the gated prepare and the SwiGLU epilogue,
+    elementwise over f32 ``x`` into ``out`` (a check of the kernels' numerics)."""
+    n = int(x.numel()) if count is None else int(count)
+    px = _buf(x, "x", torch.float32, n)
+    po = _buf(out, "out", torch.float32, n)
+    check(lib().k2w8_sigmoid_f32(_stream(stream), n, px, po))
+
+
 def rope_qknorm_f16(qkv, q_scale, k_scale, cos, sin, q_out, k_out, v_out, *, row_stride,
                     q_heads, kv_heads, k_offset, eps, tokens=None, stream=None):
     """Per-head RMSNorm (multiplier 1 + scale) and rotary embedding of q and k, v copied.

@@ -25,8 +25,8 @@ float ora_bf16_to_f32(uint16_t b);
 uint16_t ora_f16_from_f32(float x);
 float ora_f16_to_f32(uint16_t h);
 
-/* The sigmoid's exponential: a fixed f32 operation sequence shared bit-for-bit
- * with the device code. */
+/* The sigmoid's exponential: a fixed f32 function that the device code computes
+ * bit-for-bit. */
 float ora_expf(float x);
 
 /* Element-wise helpers exposed so tests can check them in bulk. */

@@ -145,6 +145,16 @@ def test_transport_rejects_a_bad_direction_count_or_alignment(k2):
         assert fragment in lib.k2w8_last_error().decode()
 
 
+def test_sigmoid_rejects_a_bad_count_or_buffer(k2):
+    lib = k2.lib()
+    odd = ctypes.c_void_p(0x10002)
+    cases = [(0, FAKE, FAKE, "count"), (1 << 32, FAKE, FAKE, "count"),
+             (16, None, FAKE, "null"), (16, odd, FAKE, "aligned")]
+    for count, x, out, fragment in cases:
+        assert lib.k2w8_sigmoid_f32(None, count, x, out) == -1, count
+        assert fragment in lib.k2w8_last_error().decode()
+
+
 def test_quantized_forward_validates_before_any_launch(k2):
     lib = k2.lib()
     cfg = k2._lib.QuantizedCfg(6144, 128, 6144)

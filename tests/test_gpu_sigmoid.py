@@ -1,0 +1,64 @@
+"""The device sigmoid of the gated prepare (kernels/prepare_gated_i8.loom:97-101) and the
+SwiGLU epilogue (kernels/gemm_i8_swiglu_256.loom:649-652) against its CPU definition,
+1 / (1 + exp(-g)) with the oracle's exp and an IEEE f32 division, bit for bit.
+
+The device evaluates the same function by other steps: the exponential's special cases
+are selected instead of branched around, and the division is the hardware reciprocal
+plus one fma correction (the IEEE division only where 1 + exp(-g) >= 2^126, whose
+quotients are subnormal). The inputs cover the whole f32 range at a fine stride, every
+value in the bands where those steps change (the cutoffs of the exponential, the
+switch to the division, subnormal quotients, overflow to infinity) and the specials.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_common import k2, sync
+
+pytestmark = pytest.mark.gpu
+
+
+def cpu_sigmoid(g: np.ndarray) -> np.ndarray:
+    g = np.asarray(g, np.float32)
+    with np.errstate(over="ignore", divide="ignore", invalid="ignore"):
+        e = oracle.expf(np.float32(0.0) - g)
+        return np.float32(1.0) / (np.float32(1.0) + e)
+
+
+def band(lo: float, hi: float) -> np.ndarray:
+    """Every f32 from lo to hi (same sign, |lo| <= |hi|)."""
+    a = np.array([lo, hi], np.float32).view(np.uint32)
+    return np.arange(min(a), max(a) + 1, dtype=np.uint32).view(np.float32)
+
+
+def inputs() -> np.ndarray:
+    stride = np.arange(0, 1 << 32, 251, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    parts = [
+        stride,
+        band(-87.0, -88.0),     # 1 + exp(-g) crosses 2^126: reciprocal -> division
+        band(-103.5, -104.5),   # exp(-g) overflows to infinity
+        band(88.5, 89.0),       # exp(-g) underflows to zero (cutoff -103.97 of -g)
+        band(-0.01, -0.02), band(0.01, 0.02),
+        np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-45, -1e-45, 3.4028235e38,
+                  -3.4028235e38], np.float32),
+    ]
+    return np.concatenate(parts)
+
+
+def test_device_sigmoid_is_bit_identical_to_the_cpu_definition():
+    x = inputs()
+    want = cpu_sigmoid(x)
+    xd = torch.from_numpy(x).cuda()
+    out = torch.empty_like(xd)
+    k2.sigmoid_f32(xd, out)
+    sync()
+    got = out.cpu().numpy()
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    diff = got.view(np.uint32)[~nan] != want.view(np.uint32)[~nan]
+    assert not diff.any(), (int(diff.sum()), x[~nan][diff][:8], got[~nan][diff][:8],
+                            want[~nan][diff][:8])
+    # the bands above do reach the division path and subnormal quotients
+    assert (want[~nan] < np.float32(2.0 ** -126)).any() and (want == 0).any()
