@@ -538,6 +538,16 @@ constexpr int64_t kTailCost = K2W8_TAIL_COST;
 #endif
 constexpr bool kUse192 = K2W8_USE_192;
 constexpr int kMidWm = K2W8_MID_WM, kMidWn = 8 / kMidWm;
+// Stages of the 64x64 tiles: four (64 KiB, two workgroups per CU) keep three K steps
+// in flight, which the short per-tile work of the mid-M shapes needs (QKV at M=256:
+// 16.1 -> 9.7 us). The 128x128 tiles keep two: more would cost them occupancy.
+#ifndef K2W8_S64_STAGES
+#define K2W8_S64_STAGES 4
+#endif
+#ifndef K2W8_S128_STAGES
+#define K2W8_S128_STAGES 2
+#endif
+constexpr int kS64Stages = K2W8_S64_STAGES, kS128Stages = K2W8_S128_STAGES;
 
 int device_cus() {
   static int cached[64];
@@ -569,8 +579,9 @@ hipError_t configure_gemm_lds() {
   hipError_t e = gemm::set_lds_tile<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>();
   if (e == hipSuccess) e = gemm::set_lds_tile<256, 192, 4, 2, 128, 2>();
   if (e == hipSuccess) e = gemm::set_lds_tile<256, 128, kMidWm, kMidWn, 128, 2>();
-  if (e == hipSuccess) e = gemm::set_lds_tile<128, 128, 2, 2, 128, 2>();
-  if (e == hipSuccess) e = gemm::set_lds_tile<64, 64, 2, 2, 128, 2>();
+  if (e == hipSuccess) e = gemm::set_lds_tile<128, 128, 2, 2, 128, kS128Stages>();
+  if (e == hipSuccess) e = gemm::set_lds_tile<64, 64, 2, 2, 128, kS64Stages>();
+  if (e == hipSuccess) e = configure_skinny_lds();
   return e;
 }
 
@@ -600,7 +611,7 @@ int splitk_steps(const GemmLaunch &l, int64_t cus) {
 // gives every CU a workgroup; 64x64 for K up to 4096; split K over 128x128 tiles when
 // those cover at most half the CUs; else 64x64.
 hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &l) {
-  if (l.m <= kSkinnyMaxTokens) return launch_skinny(epilogue, stream, l);
+  if (l.m <= kSkinnyMaxTokens || skinny_streams(epilogue, l)) return launch_skinny(epilogue, stream, l);
   gemm::GemmArgs a = gemm::args_of(l, epilogue);
   auto tiles = [&](int64_t bm, int64_t bn) { return ((l.m + bm - 1) / bm) * (l.n / bn); };
   const int64_t kCus = device_cus();
@@ -640,15 +651,15 @@ hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &l) {
     const int64_t out_col = epilogue == kEpiSwiglu ? n_big / 2 : n_big;
     const int64_t elem = epilogue == kEpiAcc ? 4 : 2;
     tail.c = static_cast<char *>(a.c) + out_col * elem;
-    return gemm::launch_tile<128, 128, 2, 2, 128, 2>(epilogue, stream, tail);
+    return gemm::launch_tile<128, 128, 2, 2, 128, kS128Stages>(epilogue, stream, tail);
   }
   if (tiles(256, 128) >= kCus)
     return gemm::launch_tile<256, 128, kMidWm, kMidWn, 128, 2>(epilogue, stream, a);
-  if (tiles(128, 128) >= kCus) return gemm::launch_tile<128, 128, 2, 2, 128, 2>(epilogue, stream, a);
+  if (tiles(128, 128) >= kCus) return gemm::launch_tile<128, 128, 2, 2, 128, kS128Stages>(epilogue, stream, a);
   // 64x64 tiles read every operand byte 4x as often as 128x128 ones: past K=4096 the
   // split-K pass over 128x128 tiles moves fewer bytes.
   if (tiles(64, 64) >= kCus && l.k <= 4096)
-    return gemm::launch_tile<64, 64, 2, 2, 128, 2>(epilogue, stream, a);
+    return gemm::launch_tile<64, 64, 2, 2, 128, kS64Stages>(epilogue, stream, a);
   const int per = splitk_steps(l, kCus);
   if (per > 0) {
     int32_t *parts = static_cast<int32_t *>(splitk_workspace(stream));
@@ -659,12 +670,12 @@ hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &l) {
       p.ldc = (int)l.n;
       p.k_split_steps = per;
       p.split_stride = l.m * l.n;
-      hipError_t e = gemm::launch_tile<128, 128, 2, 2, 128, 2>(kEpiAcc, stream, p);
+      hipError_t e = gemm::launch_tile<128, 128, 2, 2, 128, kS128Stages>(kEpiAcc, stream, p);
       if (e != hipSuccess) return e;
       return launch_splitk_reduce(epilogue, stream, parts, splits, l.m * l.n, a);
     }
   }
-  return gemm::launch_tile<64, 64, 2, 2, 128, 2>(epilogue, stream, a);
+  return gemm::launch_tile<64, 64, 2, 2, 128, kS64Stages>(epilogue, stream, a);
 }
 #endif
 

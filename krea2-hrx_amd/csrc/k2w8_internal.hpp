@@ -34,8 +34,10 @@ struct GemmLaunch {
 
 hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &g);
 // Few-token kernel (any m; chosen by launch_gemm for small m).
+bool skinny_streams(int epilogue, const GemmLaunch &g);
 hipError_t launch_skinny(int epilogue, hipStream_t stream, const GemmLaunch &g);
 hipError_t configure_gemm_lds();
+hipError_t configure_skinny_lds();
 
 // bf16 <-> f16 transport: direction 1 bf16 -> f16, 2 f16 -> bf16.
 hipError_t launch_sigmoid(hipStream_t stream, int64_t count, const float *x, float *out);

@@ -1,17 +1,16 @@
 // INT8 GEMM family for few tokens (the text-encoder-shaped regime, M <= 64 per token
 // group), where the weights dominate HBM traffic and the MFMAs are nearly idle.
 //
-// One workgroup owns RB weight rows (16 or 32: a SwiGLU gate|up pair) and a group of
-// up to 64 tokens (TB blocks of 16). Its WAVES waves split K into contiguous ranges;
-// each wave streams its range of the weight rows and token rows straight from global
-// memory into registers (no LDS staging: every weight byte is used by one MFMA per
-// token block), keeping several 64-byte K steps in flight while it computes on
-// v_mfma_i32_16x16x64_i8. The waves' int32 partial sums meet in LDS (integer
-// addition: the order is irrelevant, the result exact), and each wave then runs the
-// dequantising epilogue for one token block.
+// One workgroup owns RB weight rows (8, 16, or 32: a SwiGLU gate|up pair) and a group
+// of up to 64 tokens (TB blocks of 16). Its waves split K into contiguous ranges; each
+// wave streams its range of weight and token rows global -> LDS through a ring of its
+// own (several 128-byte K steps in flight, every transfer whole cache lines) and reads
+// the fragments of v_mfma_i32_16x16x64_i8 back from it. The waves' int32 partial sums
+// meet in LDS (integer addition: the order is irrelevant, the result exact), and wave w
+// runs the dequantising epilogue for token block w.
 //
-// Each 64-byte K step is one MFMA per (row block, token block): lane (r, kq) supplies
-// bytes [16 kq, 16 kq + 16) of row r for both operands.
+// Each 64-byte half of a K step is one MFMA per (row block, token block): lane (r, kq)
+// supplies bytes [16 kq, 16 kq + 16) of row r for both operands.
 //
 // Results are identical to the large-tile kernels' (same int32 accumulators, same
 // epilogue arithmetic): kernels/gemm_i8_256.loom:606-626 and its residual and SwiGLU
@@ -19,6 +18,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "k2w8_gemm_common.hpp"
 #include "k2w8_internal.hpp"
 #include "k2w8_numerics.hpp"
 
@@ -38,24 +38,187 @@ struct Args {
 
 constexpr int kTokensPerGroup = 64;
 
-// Epilogue of one 16-token block. With the weights as the MFMA row operand, lane
-// (t, kq) holds token t0 + t and, in register e, channel n0 + 16 rb + 4 kq + e.
-template <int EPI, int RB>
-__device__ __forceinline__ void store_block(const Args &g, const v4i (&acc)[RB / 16], int n0, int tok,
-                                            int kq) {
-  if (tok >= g.m) return;
-  const float as = (EPI == kEpiAcc) ? 1.0f : g.a_scale[tok];
+// The weight and token rows go global -> LDS through a per-wave ring of P 128-byte K
+// steps (global_load_lds_dwordx4), each transfer instruction covering 8 rows x 128
+// bytes, i.e. whole cache lines: measured on a plain read of the QKV weights, 16 rows
+// x 64 bytes per instruction (the MFMA register layout, loaded directly) took 4.3 us
+// and whole lines 3.5 us.
+// Each wave owns its ring, so the K loop needs no workgroup barrier. The epilogue's
+// per-channel and per-token operands are loaded before the K loop, so their latency
+// hides behind the weight stream instead of following it.
+//
+// RB = 8 uses half of each 16-row MFMA block (rows 8-15 repeat rows 0-7 and are not
+// stored): twice the workgroups for short-N shapes.
+template <int RB>
+struct Rows {
+  static constexpr int kBlocks = RB < 16 ? 1 : RB / 16;  // 16-row MFMA blocks
+  static constexpr int kLoads = RB / 8;                  // 8-row transfers per step
+};
+
+// Chunk swizzle of a staged 128-byte row (as in the tile kernels): 16-byte chunk c of
+// row r sits at position c ^ key(r), so one LDS cycle's rows spread over the banks.
+__device__ __forceinline__ int skey(int r) { return (r >> 1) & 7; }
+
+template <int P, int I>
+__device__ __forceinline__ void wait_steps(int newer) {
+  // Wait until at most `newer` steps (I transfers each) are still in flight.
+  if (newer >= P - 1) { gemm::wait_vmcnt<(P - 1) * I>(); return; }
+  switch (newer) {
+    case 0: gemm::wait_vmcnt<0>(); break;
+    case 1: gemm::wait_vmcnt<(P > 1 ? 1 : 0) * I>(); break;
+    case 2: gemm::wait_vmcnt<(P > 2 ? 2 : 0) * I>(); break;
+    case 3: gemm::wait_vmcnt<(P > 3 ? 3 : 0) * I>(); break;
+    case 4: gemm::wait_vmcnt<(P > 4 ? 4 : 0) * I>(); break;
+    case 5: gemm::wait_vmcnt<(P > 5 ? 5 : 0) * I>(); break;
+    case 6: gemm::wait_vmcnt<(P > 6 ? 6 : 0) * I>(); break;
+    default: gemm::wait_vmcnt<0>(); break;
+  }
+}
+
+// AR: token rows staged per token block, 16, or 8 for at most 8 tokens (MFMA columns
+// 8-15 then repeat columns 0-7 and are not stored).
+template <int TB, int AR>
+constexpr int token_loads() { return TB * AR / 8; }
+
+template <int RB, int TB, int AR, int WAVES, int P, int EPI>
+__global__ __launch_bounds__(WAVES * 64) void stream_kernel(Args g) {
+  static_assert(P >= 2 && P <= 8, "ring depth");
+  static_assert(AR == 16 || (AR == 8 && TB == 1), "token rows");
+  constexpr int RBK = Rows<RB>::kBlocks, WL = Rows<RB>::kLoads;
+  constexpr int I = WL + token_loads<TB, AR>();  // transfers per step: weights, then tokens
+  constexpr int kStep = I * 1024;      // LDS bytes per step
+  constexpr int kA = WL * 1024;        // token rows' offset within a step
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, kq = lane >> 4;
+  const int n0 = blockIdx.x * RB;
+  const int t0 = blockIdx.y * kTokensPerGroup;
+
+  // Epilogue operands, loaded now. Lane (r, kq) of wave w < TB finishes token
+  // t0 + 16w + r, channels n0 + 16 rb + 4 kq + e (SwiGLU: rb 0 gates, rb 1 ups).
+  const int tok = t0 + 16 * wave + r;
+  const bool stores = wave < TB && tok < g.m && (RB >= 16 || kq < 2) && (AR == 16 || r < 8);
+  float4 ws[RBK], gs[RBK];
+  uint2 prior[RBK], bias[RBK];
+  float as = 0.0f;
+  if (stores) {
+    as = (EPI == kEpiAcc) ? 1.0f : g.a_scale[tok];
+#pragma unroll
+    for (int rb = 0; rb < RBK; ++rb) {
+      const int nb = n0 + 16 * rb + 4 * kq;
+      if (EPI != kEpiAcc) ws[rb] = *reinterpret_cast<const float4 *>(g.w_scale + nb);
+      if (EPI == kEpiResid) {
+        gs[rb] = *reinterpret_cast<const float4 *>(g.gate + nb);
+        prior[rb] = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(g.c) + (int64_t)tok * g.n + nb);
+      }
+      if (EPI == kEpiBias) bias[rb] = *reinterpret_cast<const uint2 *>(g.bias + nb);
+    }
+  }
+
+  // This wave's K range in 128-byte steps.
+  const int steps = g.k >> 7;
+  const int lo = steps * wave / WAVES, hi = steps * (wave + 1) / WAVES;
+  const int count = hi - lo;
+  const uint32_t ring = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + wave * (P * kStep);
+
+  // Transfer i of a step covers 8 staged rows: weights (i < WL), then token rows.
+  // Lane l brings logical chunk (l & 7) ^ key(row) of row (l >> 3), so staged position
+  // l & 7 holds it.
+  uint32_t off[I];
+  const int8_t *src[I];
+#pragma unroll
+  for (int i = 0; i < I; ++i) {
+    const int row = (i < WL ? 8 * i : 8 * (i - WL)) + (lane >> 3);
+    const int c = (lane & 7) ^ skey(row);
+    if (i < WL) {
+      src[i] = g.w;
+      off[i] = (uint32_t)(n0 + row) * (uint32_t)g.lda + lo * 128 + c * 16;
+    } else {
+      src[i] = g.a;
+      off[i] = (uint32_t)min(t0 + row, g.m - 1) * (uint32_t)g.lda + lo * 128 + c * 16;
+    }
+  }
+  auto issue = [&](int st) {  // step lo + st into slot st % P
+    const uint32_t base = ring + (uint32_t)((st % P) * kStep);
+#pragma unroll
+    for (int i = 0; i < I; ++i) gemm::dma16(base + i * 1024, src[i], off[i] + st * 128);
+  };
+#pragma unroll
+  for (int p = 0; p < P; ++p)
+    if (p < count) issue(p);
+
+  // Fragment offsets within a step: row block rb, token block tb, K half h, chunk kq.
+  int w_off[RBK][2], a_off[TB][2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int rb = 0; rb < RBK; ++rb) {
+      const int row = RB < 16 ? (r & 7) : 16 * rb + r;
+      w_off[rb][h] = row * 128 + (((4 * h + kq) ^ skey(row)) << 4);
+    }
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      const int row = AR == 16 ? 16 * tb + r : (r & 7);
+      a_off[tb][h] = kA + row * 128 + (((4 * h + kq) ^ skey(row)) << 4);
+    }
+  }
+
+  v4i acc[RBK][TB];
+#pragma unroll
+  for (int rb = 0; rb < RBK; ++rb)
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) acc[rb][tb] = v4i{0, 0, 0, 0};
+
+  for (int st = 0; st < count; ++st) {
+    wait_steps<P, I>(min(count - 1 - st, P - 1));
+    const uint8_t *slot = smem + wave * (P * kStep) + (st % P) * kStep;
+    v4i wf[2][RBK], af[2][TB];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int rb = 0; rb < RBK; ++rb) wf[h][rb] = *reinterpret_cast<const v4i *>(slot + w_off[rb][h]);
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) af[h][tb] = *reinterpret_cast<const v4i *>(slot + a_off[tb][h]);
+    }
+    // The slot is free once these reads have returned: refill it with step st + P.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (st + P < count) issue(st + P);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int rb = 0; rb < RBK; ++rb)
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb)
+          acc[rb][tb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[h][rb], af[h][tb], acc[rb][tb], 0, 0, 0);
+  }
+
+  // Combine the waves' partial sums (the rings are done: reuse their LDS); wave w
+  // finishes token block w.
+  __syncthreads();
+  v4i *partial = reinterpret_cast<v4i *>(smem);  // [WAVES][RBK][TB][64]
+#pragma unroll
+  for (int rb = 0; rb < RBK; ++rb)
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) partial[((wave * RBK + rb) * TB + tb) * 64 + lane] = acc[rb][tb];
+  __syncthreads();
+  if (!stores) return;
+  v4i sum[RBK];
+#pragma unroll
+  for (int rb = 0; rb < RBK; ++rb) {
+    sum[rb] = partial[(rb * TB + wave) * 64 + lane];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) sum[rb] += partial[((w * RBK + rb) * TB + wave) * 64 + lane];
+  }
   if (EPI == kEpiSwiglu) {
-    // rb 0: gate channels n0 + 4kq + e; rb 1: the matching ups, 16 rows further on.
-    const float4 gs = *reinterpret_cast<const float4 *>(g.w_scale + n0 + 4 * kq);
-    const float4 us = *reinterpret_cast<const float4 *>(g.w_scale + n0 + 16 + 4 * kq);
-    const float gsv[4] = {gs.x, gs.y, gs.z, gs.w}, usv[4] = {us.x, us.y, us.z, us.w};
+    const float gsv[4] = {ws[0].x, ws[0].y, ws[0].z, ws[0].w};
+    const float usv[4] = {ws[RBK - 1].x, ws[RBK - 1].y, ws[RBK - 1].z, ws[RBK - 1].w};
     uint32_t packed[2];
 #pragma unroll
     for (int e = 0; e < 4; e += 2) {
-      float g0 = ((float)acc[0][e] * gsv[e]) * as, g1 = ((float)acc[0][e + 1] * gsv[e + 1]) * as;
-      float u0 = ((float)acc[RB / 16 - 1][e] * usv[e]) * as;
-      float u1 = ((float)acc[RB / 16 - 1][e + 1] * usv[e + 1]) * as;
+      float g0 = ((float)sum[0][e] * gsv[e]) * as, g1 = ((float)sum[0][e + 1] * gsv[e + 1]) * as;
+      float u0 = ((float)sum[RBK - 1][e] * usv[e]) * as;
+      float u1 = ((float)sum[RBK - 1][e + 1] * usv[e + 1]) * as;
       bf16_round2(g0, g1);
       bf16_round2(u0, u1);
       float s0 = g0 * sigmoid(g0), s1 = g1 * sigmoid(g1);
@@ -69,32 +232,26 @@ __device__ __forceinline__ void store_block(const Args &g, const v4i (&acc)[RB /
     return;
   }
 #pragma unroll
-  for (int rb = 0; rb < RB / 16; ++rb) {
+  for (int rb = 0; rb < RBK; ++rb) {
     const int nb = n0 + 16 * rb + 4 * kq;
     if (EPI == kEpiAcc) {
-      *reinterpret_cast<v4i *>(static_cast<int32_t *>(g.c) + (int64_t)tok * g.n + nb) = acc[rb];
+      *reinterpret_cast<v4i *>(static_cast<int32_t *>(g.c) + (int64_t)tok * g.n + nb) = sum[rb];
       continue;
     }
-    const float4 ws4 = *reinterpret_cast<const float4 *>(g.w_scale + nb);
-    const float ws[4] = {ws4.x, ws4.y, ws4.z, ws4.w};
+    const float wsv[4] = {ws[rb].x, ws[rb].y, ws[rb].z, ws[rb].w};
     float extra[4] = {0.f, 0.f, 0.f, 0.f};
     if (EPI == kEpiResid) {
-      const float4 v = *reinterpret_cast<const float4 *>(g.gate + nb);
-      extra[0] = v.x; extra[1] = v.y; extra[2] = v.z; extra[3] = v.w;
+      extra[0] = gs[rb].x; extra[1] = gs[rb].y; extra[2] = gs[rb].z; extra[3] = gs[rb].w;
     }
     if (EPI == kEpiBias) {
-      const uint2 v = *reinterpret_cast<const uint2 *>(g.bias + nb);
-      extra[0] = f16_value(v.x & 0xffffu); extra[1] = f16_value(v.x >> 16);
-      extra[2] = f16_value(v.y & 0xffffu); extra[3] = f16_value(v.y >> 16);
+      extra[0] = f16_value(bias[rb].x & 0xffffu); extra[1] = f16_value(bias[rb].x >> 16);
+      extra[2] = f16_value(bias[rb].y & 0xffffu); extra[3] = f16_value(bias[rb].y >> 16);
     }
-    uint16_t *out = static_cast<uint16_t *>(g.c) + (int64_t)tok * g.n + nb;
-    uint2 prior = make_uint2(0, 0);
-    if (EPI == kEpiResid) prior = *reinterpret_cast<const uint2 *>(out);
-    const uint32_t pw[2] = {prior.x, prior.y};
+    const uint32_t pw[2] = {EPI == kEpiResid ? prior[rb].x : 0u, EPI == kEpiResid ? prior[rb].y : 0u};
     uint32_t packed[2];
 #pragma unroll
     for (int e = 0; e < 4; e += 2) {
-      float v0 = ((float)acc[rb][e] * ws[e]) * as, v1 = ((float)acc[rb][e + 1] * ws[e + 1]) * as;
+      float v0 = ((float)sum[rb][e] * wsv[e]) * as, v1 = ((float)sum[rb][e + 1] * wsv[e + 1]) * as;
       if (EPI == kEpiBias) {
         v0 = v0 + extra[e];
         v1 = v1 + extra[e + 1];
@@ -109,112 +266,120 @@ __device__ __forceinline__ void store_block(const Args &g, const v4i (&acc)[RB /
         packed[e >> 1] = f16_pack2(v0, v1);
       }
     }
+    uint16_t *out = static_cast<uint16_t *>(g.c) + (int64_t)tok * g.n + nb;
     *reinterpret_cast<uint2 *>(out) = make_uint2(packed[0], packed[1]);
   }
 }
 
-template <int RB, int TB, int WAVES, int EPI>
-__global__ __launch_bounds__(WAVES * 64) void skinny_kernel(Args g) {
-  __shared__ v4i partial[WAVES][RB / 16][TB][64];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int r = lane & 15, kq = lane >> 4;
-  const int n0 = blockIdx.x * RB;
-  const int t0 = blockIdx.y * kTokensPerGroup;
+template <int RB, int TB, int AR, int WAVES, int P>
+struct StreamConfig {
+  static constexpr size_t kLds = (size_t)WAVES * P * (Rows<RB>::kLoads + token_loads<TB, AR>()) * 1024;
+};
 
-  // This wave's K range, in 64-byte steps; lane (r, kq) loads bytes [16 kq, 16 kq + 16)
-  // of each step for its weight rows and token rows.
-  const int steps = g.k >> 6;
-  const int s_lo = steps * wave / WAVES, s_hi = steps * (wave + 1) / WAVES;
-  const int count = s_hi - s_lo;
-
-  const int8_t *wrow[RB / 16];
-  const int8_t *arow[TB];
-#pragma unroll
-  for (int rb = 0; rb < RB / 16; ++rb)
-    wrow[rb] = g.w + (int64_t)(n0 + 16 * rb + r) * g.lda + s_lo * 64 + kq * 16;
-#pragma unroll
-  for (int tb = 0; tb < TB; ++tb)
-    arow[tb] = g.a + (int64_t)min(t0 + 16 * tb + r, g.m - 1) * g.lda + s_lo * 64 + kq * 16;
-
-  v4i acc[RB / 16][TB];
-#pragma unroll
-  for (int rb = 0; rb < RB / 16; ++rb)
-#pragma unroll
-    for (int tb = 0; tb < TB; ++tb) acc[rb][tb] = v4i{0, 0, 0, 0};
-
-  // A ring of P steps in flight: the loads of step i+P are issued as step i computes,
-  // so each wave keeps P steps of its rows outstanding (the weights stream from HBM).
-  constexpr int P = (RB / 16 + TB) <= 3 ? 8 : 4;
-  v4i wf[P][RB / 16], af[P][TB];
-#pragma unroll
-  for (int p = 0; p < P; ++p) {
-    if (p < count) {
-#pragma unroll
-      for (int rb = 0; rb < RB / 16; ++rb) wf[p][rb] = *reinterpret_cast<const v4i *>(wrow[rb] + p * 64);
-#pragma unroll
-      for (int tb = 0; tb < TB; ++tb) af[p][tb] = *reinterpret_cast<const v4i *>(arow[tb] + p * 64);
-    }
-  }
-  for (int base = 0; base < count; base += P) {
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-      const int st = base + p;
-      if (st < count) {
-#pragma unroll
-        for (int rb = 0; rb < RB / 16; ++rb)
-#pragma unroll
-          for (int tb = 0; tb < TB; ++tb)
-            acc[rb][tb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[p][rb], af[p][tb], acc[rb][tb], 0, 0, 0);
-        if (st + P < count) {
-#pragma unroll
-          for (int rb = 0; rb < RB / 16; ++rb)
-            wf[p][rb] = *reinterpret_cast<const v4i *>(wrow[rb] + (st + P) * 64);
-#pragma unroll
-          for (int tb = 0; tb < TB; ++tb)
-            af[p][tb] = *reinterpret_cast<const v4i *>(arow[tb] + (st + P) * 64);
-        }
-      }
-    }
-  }
-
-  // Combine the waves' partial sums; wave w finishes token block w.
-#pragma unroll
-  for (int rb = 0; rb < RB / 16; ++rb)
-#pragma unroll
-    for (int tb = 0; tb < TB; ++tb) partial[wave][rb][tb][lane] = acc[rb][tb];
-  __syncthreads();
-  if (wave < TB) {
-    v4i sum[RB / 16];
-#pragma unroll
-    for (int rb = 0; rb < RB / 16; ++rb) {
-      sum[rb] = partial[0][rb][wave][lane];
-#pragma unroll
-      for (int w = 1; w < WAVES; ++w) sum[rb] += partial[w][rb][wave][lane];
-    }
-    store_block<EPI, RB>(g, sum, n0, t0 + 16 * wave + r, kq);
-  }
-}
-
-template <int RB, int TB, int WAVES>
-hipError_t launch_rb(int epi, hipStream_t stream, const Args &a) {
+template <int RB, int TB, int AR, int WAVES, int P>
+hipError_t launch_stream(int epi, hipStream_t stream, const Args &a) {
+  constexpr size_t lds = StreamConfig<RB, TB, AR, WAVES, P>::kLds;
+  static_assert(lds <= 160 * 1024, "LDS");
   dim3 grid(a.n / RB, (a.m + kTokensPerGroup - 1) / kTokensPerGroup), block(WAVES * 64);
   switch (epi) {
-    case kEpiPlain: hipLaunchKernelGGL((skinny_kernel<RB, TB, WAVES, kEpiPlain>), grid, block, 0, stream, a); break;
-    case kEpiResid: hipLaunchKernelGGL((skinny_kernel<RB, TB, WAVES, kEpiResid>), grid, block, 0, stream, a); break;
-    case kEpiSwiglu: hipLaunchKernelGGL((skinny_kernel<RB, TB, WAVES, kEpiSwiglu>), grid, block, 0, stream, a); break;
-    case kEpiBias: hipLaunchKernelGGL((skinny_kernel<RB, TB, WAVES, kEpiBias>), grid, block, 0, stream, a); break;
-    default: hipLaunchKernelGGL((skinny_kernel<RB, TB, WAVES, kEpiAcc>), grid, block, 0, stream, a); break;
+    case kEpiPlain: hipLaunchKernelGGL((stream_kernel<RB, TB, AR, WAVES, P, kEpiPlain>), grid, block, lds, stream, a); break;
+    case kEpiResid: hipLaunchKernelGGL((stream_kernel<RB, TB, AR, WAVES, P, kEpiResid>), grid, block, lds, stream, a); break;
+    case kEpiSwiglu: hipLaunchKernelGGL((stream_kernel<RB, TB, AR, WAVES, P, kEpiSwiglu>), grid, block, lds, stream, a); break;
+    case kEpiBias: hipLaunchKernelGGL((stream_kernel<RB, TB, AR, WAVES, P, kEpiBias>), grid, block, lds, stream, a); break;
+    default: hipLaunchKernelGGL((stream_kernel<RB, TB, AR, WAVES, P, kEpiAcc>), grid, block, lds, stream, a); break;
   }
   return hipGetLastError();
 }
 
-template <int TB>
+template <int RB, int TB, int AR, int WAVES, int P>
+hipError_t set_lds_stream() {
+  constexpr size_t lds = StreamConfig<RB, TB, AR, WAVES, P>::kLds;
+  const void *fns[5] = {reinterpret_cast<const void *>(stream_kernel<RB, TB, AR, WAVES, P, kEpiPlain>),
+                        reinterpret_cast<const void *>(stream_kernel<RB, TB, AR, WAVES, P, kEpiResid>),
+                        reinterpret_cast<const void *>(stream_kernel<RB, TB, AR, WAVES, P, kEpiSwiglu>),
+                        reinterpret_cast<const void *>(stream_kernel<RB, TB, AR, WAVES, P, kEpiBias>),
+                        reinterpret_cast<const void *>(stream_kernel<RB, TB, AR, WAVES, P, kEpiAcc>)};
+  for (const void *f : fns) {
+    hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+#ifndef K2W8_SK_WAVES
+#define K2W8_SK_WAVES 4
+#endif
+#ifndef K2W8_SK_LDS_KB
+#define K2W8_SK_LDS_KB 48
+#endif
+#ifndef K2W8_SK_PMAX
+#define K2W8_SK_PMAX 8
+#endif
+constexpr int kWaves = K2W8_SK_WAVES;
+
+// Ring depth: as many steps as fit the LDS budget per workgroup (at least 2).
+constexpr int ring_depth_of(int rb, int tb, int ar) {
+  const int per_step = kWaves * (rb / 8 + tb * ar / 8);  // KiB
+  const int p = K2W8_SK_LDS_KB / per_step;
+  return p < 2 ? 2 : (p > K2W8_SK_PMAX ? K2W8_SK_PMAX : p);
+}
+template <int RB, int TB, int AR>
+constexpr int ring_depth() { return ring_depth_of(RB, TB, AR); }
+
+// Weight rows per workgroup: a gate|up pair for SwiGLU; else 16, or 8 when 16-row
+// workgroups would leave CUs idle.
+int rows_of(int epi, int64_t n) {
+  if (epi == kEpiSwiglu) return 32;
+  return n / 16 < device_cus() ? 8 : 16;
+}
+
+template <int RB, int TB, int AR>
+hipError_t launch_rows(int epi, hipStream_t stream, const Args &a) {
+  return launch_stream<RB, TB, AR, kWaves, ring_depth<RB, TB, AR>()>(epi, stream, a);
+}
+
+template <int TB, int AR>
 hipError_t launch_tb(int epi, hipStream_t stream, const Args &a) {
-  if (epi == kEpiSwiglu) return launch_rb<32, TB, 4>(epi, stream, a);
-  return launch_rb<16, TB, 4>(epi, stream, a);
+  switch (rows_of(epi, a.n)) {
+    case 32: return launch_rows<32, TB, AR>(epi, stream, a);
+    case 8: return launch_rows<8, TB, AR>(epi, stream, a);
+    default: return launch_rows<16, TB, AR>(epi, stream, a);
+  }
+}
+
+template <int TB, int AR>
+hipError_t set_lds_tb() {
+  hipError_t e = set_lds_stream<32, TB, AR, kWaves, ring_depth<32, TB, AR>()>();
+  if (e == hipSuccess) e = set_lds_stream<16, TB, AR, kWaves, ring_depth<16, TB, AR>()>();
+  if (e == hipSuccess) e = set_lds_stream<8, TB, AR, kWaves, ring_depth<8, TB, AR>()>();
+  return e;
 }
 
 }  // namespace skinny
+
+// Past kSkinnyMaxTokens the streaming kernel still wins while K is short and its
+// grid (one workgroup per RB weight rows and per 64 tokens) is resident at once:
+// measured at K=2560, N=4096, M=64-128: 12-15 -> 7-9 us; where the grid takes two
+// rounds (N=19456, M=64) or K is long (9728), the tile kernels are faster.
+bool skinny_streams(int epilogue, const GemmLaunch &l) {
+  if (l.m > 128 || l.k > 4096) return false;
+  const int64_t tokens = l.m < skinny::kTokensPerGroup ? l.m : skinny::kTokensPerGroup;
+  const int tb = (int)((tokens + 15) / 16), ar = tokens <= 8 ? 8 : 16;
+  const int rb = skinny::rows_of(epilogue, l.n);
+  const int lds_kb = skinny::kWaves * skinny::ring_depth_of(rb, tb, ar) * (rb / 8 + tb * ar / 8);
+  const int64_t per_cu = 160 / lds_kb;
+  const int64_t grid = (l.n / rb) * ((l.m + skinny::kTokensPerGroup - 1) / skinny::kTokensPerGroup);
+  return grid <= per_cu * device_cus();
+}
+
+hipError_t configure_skinny_lds() {
+  hipError_t e = skinny::set_lds_tb<1, 8>();
+  if (e == hipSuccess) e = skinny::set_lds_tb<1, 16>();
+  if (e == hipSuccess) e = skinny::set_lds_tb<2, 16>();
+  if (e == hipSuccess) e = skinny::set_lds_tb<3, 16>();
+  if (e == hipSuccess) e = skinny::set_lds_tb<4, 16>();
+  return e;
+}
 
 hipError_t launch_skinny(int epilogue, hipStream_t stream, const GemmLaunch &l) {
   skinny::Args a;
@@ -230,11 +395,14 @@ hipError_t launch_skinny(int epilogue, hipStream_t stream, const GemmLaunch &l) 
   a.k = (int)l.k;
   a.lda = (int)l.lda;
   const int tokens = (int)(l.m < skinny::kTokensPerGroup ? l.m : skinny::kTokensPerGroup);
+#ifndef K2W8_SK_NO_A8
+  if (tokens <= 8) return skinny::launch_tb<1, 8>(epilogue, stream, a);
+#endif
   switch ((tokens + 15) / 16) {
-    case 1: return skinny::launch_tb<1>(epilogue, stream, a);
-    case 2: return skinny::launch_tb<2>(epilogue, stream, a);
-    case 3: return skinny::launch_tb<3>(epilogue, stream, a);
-    default: return skinny::launch_tb<4>(epilogue, stream, a);
+    case 1: return skinny::launch_tb<1, 16>(epilogue, stream, a);
+    case 2: return skinny::launch_tb<2, 16>(epilogue, stream, a);
+    case 3: return skinny::launch_tb<3, 16>(epilogue, stream, a);
+    default: return skinny::launch_tb<4, 16>(epilogue, stream, a);
   }
 }
 

@@ -106,12 +106,21 @@ SHAPES = [
     (256, 9728, 2560, 0),
     (129, 2560, 4096, 64),
     (300, 1024, 512, 0),
-    # few-token kernel: K ranges that leave single 64-byte steps per wave, 1..4 blocks
+    # few-token kernel: K ranges that leave a wave one 128-byte step or none; 8-row
+    # (N/16 below the CU count) and 16-row workgroups; 8 staged token rows (M <= 8) and
+    # one or two 16-token blocks; row strides that are not whole cache lines
     (2, 384, 256, 0),
     (16, 2560, 512, 0),
+    (8, 9728, 256, 64),
+    (9, 256, 4096, 0),
+    (24, 512, 4096, 64),
+    (32, 1024, 1024, 0),
     (33, 640, 384, 64),
     (64, 9728, 256, 0),
     (77, 2560, 512, 0),
+    # the streaming kernel past 32 tokens (short K, grid resident at once): two token
+    # groups of 64 and 36
+    (100, 1024, 4096, 64),
 ]
 
 
