@@ -144,7 +144,11 @@ struct Bounds {
 // kSingle: one-wave teams (no block barriers, the norm's sum of squares from
 // registers, norm factors staged in LDS). Otherwise teams of wpt waves.
 template <int kKind, int T, bool kSingle>
-__global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArgs args) {
+#ifndef K2W8_PREP_WPE
+#define K2W8_PREP_WPE 1
+#endif
+__global__ __launch_bounds__(Bounds<T>::kThreads) __attribute__((amdgpu_waves_per_eu(K2W8_PREP_WPE)))
+void prepare_kernel(PrepareArgs args) {
   constexpr bool kQuarter = (kKind == kPlain);
   __shared__ float lds_part[2][kMaxTeams][8];         // norm partials (multi-wave teams)
   __shared__ float lds_amax[2][kMaxTeams][kMaxWpt];   // wave maxima (multi-wave teams)
@@ -193,7 +197,10 @@ __global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArg
   // one-wave teams stages them in LDS once (run r at float4 slots 12 r .. 12 r + 11),
   // wider teams read them from global memory per token.
   extern __shared__ float4 factor_lds[];
-  constexpr bool kLdsFactors = (kKind == kNorm) && kSingle;
+#ifndef K2W8_PREP_LDS_FACTORS
+#define K2W8_PREP_LDS_FACTORS 1
+#endif
+  constexpr bool kLdsFactors = (kKind == kNorm) && kSingle && K2W8_PREP_LDS_FACTORS;
   if (kLdsFactors) {
     for (int c = threadIdx.x; c < (width >> 2); c += blockDim.x) {
       const float4 a = reinterpret_cast<const float4 *>(args.norm_scale)[c];
@@ -505,7 +512,10 @@ hipError_t launch_kind(hipStream_t stream, PrepareArgs a) {
   // The norm keeps rows of up to 4096 in one wave (sum of squares from registers,
   // factors in LDS); the other prepares use K2W8_PREPARE_MAX_RUNS_PER_LANE.
   int t = 1;
-  team_shape(a, kKind == kNorm ? 4 : K2W8_PREPARE_MAX_RUNS_PER_LANE, t);
+#ifndef K2W8_PREP_NORM_RUNS
+#define K2W8_PREP_NORM_RUNS 4
+#endif
+  team_shape(a, kKind == kNorm ? K2W8_PREP_NORM_RUNS : K2W8_PREPARE_MAX_RUNS_PER_LANE, t);
   if (a.wpt == 1) return launch_t<kKind, true>(t, stream, a);
   return launch_t<kKind, false>(t, stream, a);
 }
