@@ -100,6 +100,8 @@ SHAPES = [
     (4096, 256, 9216, 0),
     (4096, 128, 3072, 64),
     (2304, 128, 24576, 0),
+    # one round of 256x128 tiles over more than half the CUs: the three-stage kernel
+    (200, 1024, 19456, 64),
     # split K over 128x128 tiles (fewer than half the CUs get a tile; or 64x64 tiles
     # would fill the chip but K is long)
     (320, 4224, 4096, 0),
