@@ -61,10 +61,9 @@ __device__ __forceinline__ float f16_round(float x) { return (float)(_Float16)x;
 
 // exp(x) for the sigmoids of the gated prepare and the SwiGLU epilogue:
 // Cody-Waite reduction x = n*ln2 + r (two-part ln2), e^r = 1 + r + r^2 q(r) with a
-// degree-4 least-squares q, then 2^n as two power-of-two factors (the first product
-// is exact, the second rounds once). The CPU definition splits n as n/2 (toward zero)
-// and branches to its special cases; this form splits as floor(n/2) and selects them,
-// which gives the identical value for every f32 input.
+// degree-4 least-squares q, then p * 2^n rounded once. The CPU definition scales by
+// two power-of-two factors and branches to its special cases; this form uses ldexp
+// and selects them, which gives the identical value for every f32 input.
 __device__ __forceinline__ float sigmoid_exp(float x) {
   // Branch-free: the special cases are selected at the end (a wave would otherwise
   // branch around them per element).
@@ -77,13 +76,10 @@ __device__ __forceinline__ float sigmoid_exp(float x) {
   q = __builtin_fmaf(q, r, 0.5f);
   float r2 = r * r;
   float p = 1.0f + __builtin_fmaf(q, r2, r);
-  // p * 2^n with one rounding: p * 2^(n/2) is exact (normal), the second factor rounds.
-  int ni = (int)n;
-  int n1 = ni >> 1;
-  int n2 = ni - n1;
-  float s1 = __uint_as_float((uint32_t)(n1 + 127) << 23);
-  float s2 = __uint_as_float((uint32_t)(n2 + 127) << 23);
-  float e = (p * s1) * s2;
+  // p * 2^n with one rounding (v_ldexp_f32). The CPU definition multiplies by 2^(n/2)
+  // (exact: the product stays normal) and then by 2^(n - n/2), which rounds once: the
+  // same value.
+  float e = __builtin_amdgcn_ldexpf(p, (int)n);
   e = x > 0x1.62e42ep+6f ? __builtin_inff() : e;
   e = x < -0x1.9fe368p+6f ? 0.0f : e;
   return x != x ? x : e;

@@ -98,7 +98,7 @@ static inline float f16_round(float x) { return ora_f16_to_f32(ora_f16_from_f32(
  * 1 + r + r^2 q(r) with q a degree-4 Chebyshev-weighted least-squares fit of
  * (e^r - 1 - r)/r^2 on [-ln2/2, ln2/2], then 2^n applied as two exact power-of-two
  * factors. The device code evaluates the same function (its steps differ only in
- * ways that leave every result unchanged: a floor split of n, selected special
+ * ways that leave every result unchanged: one ldexp for 2^n, selected special
  * cases, and a corrected hardware reciprocal for 1/den); the GPU tests compare the
  * device sigmoid with this one bit for bit over the f32 range.
  */
