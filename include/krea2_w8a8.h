@@ -4,9 +4,12 @@
  * One entry point per reference kernel, with the reference's positional buffer
  * bindings in the reference's order, its compile-time configuration passed as a
  * struct (one field per `config.decl`), and its one runtime scalar (`tokens` or
- * `m_size`). Every pointer is device memory the caller owns; the library never
- * allocates. `stream` is a hipStream_t (NULL: the null stream). Calls enqueue
- * work and return; they do not synchronise.
+ * `m_size`). Every pointer is device memory the caller owns. The library allocates
+ * one thing itself: GEMMs whose output tiles would leave most CUs idle split K, and
+ * their int32 partial sums go to a 64 MiB workspace per (device, stream), allocated
+ * on the first such call outside a stream capture and kept until the process ends
+ * (under capture, without it, the call runs unsplit). `stream` is a hipStream_t
+ * (NULL: the null stream). Calls enqueue work and return; they do not synchronise.
  *
  * Data types on the buffers:
  *   f16 / bf16 activations: 16-bit IEEE half / bfloat16 bit patterns

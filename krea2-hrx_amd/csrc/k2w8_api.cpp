@@ -140,13 +140,13 @@ int k2w8_fail_runtime(const char *stage, hipError_t e) { return runtime(stage, e
 int k2w8_succeed() { return ok(); }
 // The one-time set-up of the launch paths (kernel attributes, device queries), done
 // before a stream capture so that none of it happens inside one.
-int k2w8_prime_launches() {
+int k2w8_prime_launches(void *stream) {
   int rc = ensure_configured("blocks_record");
   if (rc != K2W8_OK) return rc;
   (void)k2w8::device_cus();
-  // Allocate the split-K workspace now, outside the capture, so recorded GEMMs may
-  // split K as eager ones do.
-  (void)k2w8::splitk_workspace(nullptr);
+  // Allocate the stream's split-K workspace now, outside the capture, so recorded
+  // GEMMs may split K as eager ones do.
+  (void)k2w8::splitk_workspace(static_cast<hipStream_t>(stream));
   return K2W8_OK;
 }
 

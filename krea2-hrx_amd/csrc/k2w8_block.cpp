@@ -22,7 +22,7 @@
 int k2w8_fail_invalid(const char *message);
 int k2w8_fail_runtime(const char *stage, hipError_t e);
 int k2w8_succeed();
-int k2w8_prime_launches();
+int k2w8_prime_launches(void *stream);
 
 namespace {
 
@@ -292,7 +292,7 @@ int k2w8_blocks_record(void *stream, const k2w8_block_cfg *cfg, int64_t layers,
   if (!stream)
     return k2w8_fail_invalid("blocks_record: recording needs a created stream (not the null stream)");
   // One-time set-up (kernel attributes, device queries) must not happen inside capture.
-  int rc = k2w8_prime_launches();
+  int rc = k2w8_prime_launches(stream);
   if (rc != K2W8_OK) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);

@@ -6,12 +6,16 @@
 // (kernels/gemm_i8_256.loom:606-626, kernels/gemm_i8_resid_256.loom:623-635,
 // kernels/gemm_i8_swiglu_256.loom:640-660).
 //
-// The workspace is one device allocation per device, made on first use outside any
-// stream capture and kept for the life of the process.
+// The workspace is one device allocation per (device, stream), made on first use
+// outside any stream capture and kept for the life of the process. Calls on one
+// stream are ordered, so they may share it; calls on different streams get their own
+// and never race on it.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <map>
 #include <mutex>
+#include <utility>
 
 #include "k2w8_gemm_common.hpp"
 #include "k2w8_internal.hpp"
@@ -126,9 +130,8 @@ __global__ __launch_bounds__(256) void reduce_kernel(ReduceArgs r) {
 }
 
 constexpr size_t kWorkspaceBytes = size_t(64) << 20;
-constexpr int kMaxDevices = 64;
 std::mutex g_lock;
-void *g_workspace[kMaxDevices];
+std::map<std::pair<int, uintptr_t>, void *> g_workspace;  // (device, stream) -> buffer
 
 }  // namespace splitk
 
@@ -136,9 +139,11 @@ size_t splitk_workspace_bytes() { return splitk::kWorkspaceBytes; }
 
 void *splitk_workspace(hipStream_t stream) {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= splitk::kMaxDevices) return nullptr;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  const auto key = std::make_pair(dev, reinterpret_cast<uintptr_t>(stream));
   std::lock_guard<std::mutex> guard(splitk::g_lock);
-  if (splitk::g_workspace[dev]) return splitk::g_workspace[dev];
+  const auto it = splitk::g_workspace.find(key);
+  if (it != splitk::g_workspace.end()) return it->second;
   // Never allocate inside a stream capture: the caller then runs without split-K.
   hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
   if (stream && hipStreamIsCapturing(stream, &status) != hipSuccess) return nullptr;
@@ -148,7 +153,7 @@ void *splitk_workspace(hipStream_t stream) {
     (void)hipGetLastError();
     return nullptr;
   }
-  splitk::g_workspace[dev] = p;
+  splitk::g_workspace[key] = p;
   return p;
 }
 

@@ -226,3 +226,27 @@ def test_swiglu_reads_the_sixteen_row_interleave():
     ref_acc = oracle.gemm_i32(a, swapped, m, n, k, k)
     assert np.array_equal(other, oracle.epilogue_swiglu(ref_acc, ws_swapped, sc))
     assert not np.array_equal(base, other)
+
+
+def test_split_k_calls_on_two_streams_keep_their_own_workspace():
+    # (256, 9728, 2560) splits K: its int32 partial sums go to a workspace per stream.
+    # Two streams running such calls at the same time must each get their own results.
+    rng = np.random.default_rng(21)
+    m, k, n = 256, 9728, 2560
+    w = int8_weights(rng, n, k)
+    ws = channel_scales(rng, n)
+    inputs = [int8_weights(rng, m, k) for _ in range(2)]
+    a_scale = rng.uniform(1e-3, 3e-2, m).astype(np.float32)
+    want = [oracle.epilogue_plain(oracle.gemm_i32(a, w, m, n, k, k), ws, a_scale) for a in inputs]
+    W, WS, AS = dev(w), dev(ws), dev(a_scale)
+    A = [dev(a) for a in inputs]
+    outs = [torch.empty((m, n), dtype=torch.float16, device="cuda") for _ in range(2)]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    for _ in range(4):  # interleaved launches, so the two streams' kernels overlap
+        for i in range(2):
+            with torch.cuda.stream(streams[i]):
+                k2.gemm_i8(A[i], W, WS, AS, outs[i], cfg=cfg(k, n, k), m=m)
+    torch.cuda.synchronize()
+    for i in range(2):
+        assert np.array_equal(host(outs[i]), want[i]), i
