@@ -144,11 +144,7 @@ struct Bounds {
 // kSingle: one-wave teams (no block barriers, the norm's sum of squares from
 // registers, norm factors staged in LDS). Otherwise teams of wpt waves.
 template <int kKind, int T, bool kSingle>
-#ifndef K2W8_PREP_WPE
-#define K2W8_PREP_WPE 1
-#endif
-__global__ __launch_bounds__(Bounds<T>::kThreads) __attribute__((amdgpu_waves_per_eu(K2W8_PREP_WPE)))
-void prepare_kernel(PrepareArgs args) {
+__global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArgs args) {
   constexpr bool kQuarter = (kKind == kPlain);
   __shared__ float lds_part[2][kMaxTeams][8];         // norm partials (multi-wave teams)
   __shared__ float lds_amax[2][kMaxTeams][kMaxWpt];   // wave maxima (multi-wave teams)
@@ -197,10 +193,7 @@ void prepare_kernel(PrepareArgs args) {
   // one-wave teams stages them in LDS once (run r at float4 slots 12 r .. 12 r + 11),
   // wider teams read them from global memory per token.
   extern __shared__ float4 factor_lds[];
-#ifndef K2W8_PREP_LDS_FACTORS
-#define K2W8_PREP_LDS_FACTORS 1
-#endif
-  constexpr bool kLdsFactors = (kKind == kNorm) && kSingle && K2W8_PREP_LDS_FACTORS;
+  constexpr bool kLdsFactors = (kKind == kNorm) && kSingle;
   if (kLdsFactors) {
     for (int c = threadIdx.x; c < (width >> 2); c += blockDim.x) {
       const float4 a = reinterpret_cast<const float4 *>(args.norm_scale)[c];
@@ -509,13 +502,13 @@ hipError_t launch_t(int t, hipStream_t stream, const PrepareArgs &a) {
 
 template <int kKind>
 hipError_t launch_kind(hipStream_t stream, PrepareArgs a) {
-  // The norm keeps rows of up to 4096 in one wave (sum of squares from registers,
-  // factors in LDS); the other prepares use K2W8_PREPARE_MAX_RUNS_PER_LANE.
+  // Runs of 16 elements per lane, at most: the norm keeps rows of up to 4096 in one
+  // wave (sum of squares from registers, factors in LDS); the plain prepare takes
+  // three (fewer waves per row: 9728 wide 50.5 -> 41.8 us at M=4096); the gated one
+  // one (more waves per row: its sigmoid makes each element dearer).
+  constexpr int kRuns = kKind == kNorm ? 4 : (kKind == kPlain ? 3 : K2W8_PREPARE_MAX_RUNS_PER_LANE);
   int t = 1;
-#ifndef K2W8_PREP_NORM_RUNS
-#define K2W8_PREP_NORM_RUNS 4
-#endif
-  team_shape(a, kKind == kNorm ? K2W8_PREP_NORM_RUNS : K2W8_PREPARE_MAX_RUNS_PER_LANE, t);
+  team_shape(a, kRuns, t);
   if (a.wpt == 1) return launch_t<kKind, true>(t, stream, a);
   return launch_t<kKind, false>(t, stream, a);
 }
