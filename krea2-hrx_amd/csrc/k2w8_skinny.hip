@@ -1,8 +1,8 @@
 // INT8 GEMM family for few tokens (the text-encoder-shaped regime, M <= 64 per token
 // group), where the weights dominate HBM traffic and the MFMAs are nearly idle.
 //
-// One workgroup owns RB weight rows (8, 16, or 32: a SwiGLU gate|up pair) and a group
-// of up to 64 tokens (TB blocks of 16). Its waves split K into contiguous ranges; each
+// One workgroup owns RB weight rows (16, or 32: a SwiGLU gate|up pair) and a group of
+// up to 64 tokens (TB blocks of 16). Its waves split K into contiguous ranges; each
 // wave streams its range of weight and token rows global -> LDS through a ring of its
 // own (several 128-byte K steps in flight, every transfer whole cache lines) and reads
 // the fragments of v_mfma_i32_16x16x64_i8 back from it. The waves' int32 partial sums
@@ -46,13 +46,11 @@ constexpr int kTokensPerGroup = 64;
 // Each wave owns its ring, so the K loop needs no workgroup barrier. The epilogue's
 // per-channel and per-token operands are loaded before the K loop, so their latency
 // hides behind the weight stream instead of following it.
-//
-// RB = 8 uses half of each 16-row MFMA block (rows 8-15 repeat rows 0-7 and are not
-// stored): twice the workgroups for short-N shapes.
 template <int RB>
 struct Rows {
-  static constexpr int kBlocks = RB < 16 ? 1 : RB / 16;  // 16-row MFMA blocks
-  static constexpr int kLoads = RB / 8;                  // 8-row transfers per step
+  static_assert(RB % 16 == 0, "whole 16-row MFMA blocks");
+  static constexpr int kBlocks = RB / 16;  // 16-row MFMA blocks
+  static constexpr int kLoads = RB / 8;    // 8-row transfers per step
 };
 
 // Chunk swizzle of a staged 128-byte row (as in the tile kernels): 16-byte chunk c of
@@ -98,7 +96,7 @@ __global__ __launch_bounds__(WAVES * 64) void stream_kernel(Args g) {
   // Epilogue operands, loaded now. Lane (r, kq) of wave w < TB finishes token
   // t0 + 16w + r, channels n0 + 16 rb + 4 kq + e (SwiGLU: rb 0 gates, rb 1 ups).
   const int tok = t0 + 16 * wave + r;
-  const bool stores = wave < TB && tok < g.m && (RB >= 16 || kq < 2) && (AR == 16 || r < 8);
+  const bool stores = wave < TB && tok < g.m && (AR == 16 || r < 8);
   float4 ws[RBK], gs[RBK];
   uint2 prior[RBK], bias[RBK];
   float as = 0.0f;
@@ -154,7 +152,7 @@ __global__ __launch_bounds__(WAVES * 64) void stream_kernel(Args g) {
   for (int h = 0; h < 2; ++h) {
 #pragma unroll
     for (int rb = 0; rb < RBK; ++rb) {
-      const int row = RB < 16 ? (r & 7) : 16 * rb + r;
+      const int row = 16 * rb + r;
       w_off[rb][h] = row * 128 + (((4 * h + kq) ^ skey(row)) << 4);
     }
 #pragma unroll
@@ -306,52 +304,44 @@ hipError_t set_lds_stream() {
   return hipSuccess;
 }
 
-#ifndef K2W8_SK_WAVES
-#define K2W8_SK_WAVES 4
-#endif
 #ifndef K2W8_SK_LDS_KB
 #define K2W8_SK_LDS_KB 48
 #endif
 #ifndef K2W8_SK_PMAX
 #define K2W8_SK_PMAX 8
 #endif
-constexpr int kWaves = K2W8_SK_WAVES;
 
 // Ring depth: as many steps as fit the LDS budget per workgroup (at least 2).
-constexpr int ring_depth_of(int rb, int tb, int ar) {
-  const int per_step = kWaves * (rb / 8 + tb * ar / 8);  // KiB
+constexpr int ring_depth_of(int rb, int tb, int ar, int waves) {
+  const int per_step = waves * (rb / 8 + tb * ar / 8);  // KiB
   const int p = K2W8_SK_LDS_KB / per_step;
   return p < 2 ? 2 : (p > K2W8_SK_PMAX ? K2W8_SK_PMAX : p);
 }
-template <int RB, int TB, int AR>
-constexpr int ring_depth() { return ring_depth_of(RB, TB, AR); }
 
-// Weight rows per workgroup: a gate|up pair for SwiGLU; else 16, or 8 when 16-row
-// workgroups would leave CUs idle.
-int rows_of(int epi, int64_t n) {
-  if (epi == kEpiSwiglu) return 32;
-  return n / 16 < device_cus() ? 8 : 16;
-}
+// Workgroup shape: a gate|up pair (32 rows) for SwiGLU, else 16 rows; four waves, or
+// eight when N/16 workgroups would leave CUs idle (each wave then streams half as
+// many K steps). Measured on the down projection (N=2560, K=9728) against 8-row
+// workgroups of four waves: M=1 7.9 -> 6.8 us, M=16 11.1 -> 8.9, M=32 15.7 -> 11.3.
+int rows_of(int epi) { return epi == kEpiSwiglu ? 32 : 16; }
+int waves_of(int epi, int64_t n) { return epi != kEpiSwiglu && n / 16 < device_cus() ? 8 : 4; }
 
-template <int RB, int TB, int AR>
+template <int RB, int TB, int AR, int WAVES>
 hipError_t launch_rows(int epi, hipStream_t stream, const Args &a) {
-  return launch_stream<RB, TB, AR, kWaves, ring_depth<RB, TB, AR>()>(epi, stream, a);
+  return launch_stream<RB, TB, AR, WAVES, ring_depth_of(RB, TB, AR, WAVES)>(epi, stream, a);
 }
 
 template <int TB, int AR>
 hipError_t launch_tb(int epi, hipStream_t stream, const Args &a) {
-  switch (rows_of(epi, a.n)) {
-    case 32: return launch_rows<32, TB, AR>(epi, stream, a);
-    case 8: return launch_rows<8, TB, AR>(epi, stream, a);
-    default: return launch_rows<16, TB, AR>(epi, stream, a);
-  }
+  if (epi == kEpiSwiglu) return launch_rows<32, TB, AR, 4>(epi, stream, a);
+  if (waves_of(epi, a.n) == 8) return launch_rows<16, TB, AR, 8>(epi, stream, a);
+  return launch_rows<16, TB, AR, 4>(epi, stream, a);
 }
 
 template <int TB, int AR>
 hipError_t set_lds_tb() {
-  hipError_t e = set_lds_stream<32, TB, AR, kWaves, ring_depth<32, TB, AR>()>();
-  if (e == hipSuccess) e = set_lds_stream<16, TB, AR, kWaves, ring_depth<16, TB, AR>()>();
-  if (e == hipSuccess) e = set_lds_stream<8, TB, AR, kWaves, ring_depth<8, TB, AR>()>();
+  hipError_t e = set_lds_stream<32, TB, AR, 4, ring_depth_of(32, TB, AR, 4)>();
+  if (e == hipSuccess) e = set_lds_stream<16, TB, AR, 4, ring_depth_of(16, TB, AR, 4)>();
+  if (e == hipSuccess) e = set_lds_stream<16, TB, AR, 8, ring_depth_of(16, TB, AR, 8)>();
   return e;
 }
 
@@ -365,8 +355,8 @@ bool skinny_streams(int epilogue, const GemmLaunch &l) {
   if (l.m > 128 || l.k > 4096) return false;
   const int64_t tokens = l.m < skinny::kTokensPerGroup ? l.m : skinny::kTokensPerGroup;
   const int tb = (int)((tokens + 15) / 16), ar = tokens <= 8 ? 8 : 16;
-  const int rb = skinny::rows_of(epilogue, l.n);
-  const int lds_kb = skinny::kWaves * skinny::ring_depth_of(rb, tb, ar) * (rb / 8 + tb * ar / 8);
+  const int rb = skinny::rows_of(epilogue), waves = skinny::waves_of(epilogue, l.n);
+  const int lds_kb = waves * skinny::ring_depth_of(rb, tb, ar, waves) * (rb / 8 + tb * ar / 8);
   const int64_t per_cu = 160 / lds_kb;
   const int64_t grid = (l.n / rb) * ((l.m + skinny::kTokensPerGroup - 1) / skinny::kTokensPerGroup);
   return grid <= per_cu * device_cus();
