@@ -131,6 +131,7 @@ struct Raw {
 };
 
 constexpr int kMaxThreads = 1024;
+constexpr int kFactorStride = 13;  // float4 slots per run of staged norm factors
 constexpr int kMaxTeams = 4;
 constexpr int kMaxWpt = 16;
 
@@ -190,7 +191,9 @@ __global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArg
 
   // Norm vectors (kernels/prepare_norm_i8.loom:150-158) as the per-element factors
   // ns + 1, bf16(ms + 1) and the shift. They do not depend on the token: a block of
-  // one-wave teams stages them in LDS once (run r at float4 slots 12 r .. 12 r + 11),
+  // one-wave teams stages them in LDS once (run r at float4 slots 13 r .. 13 r + 11:
+  // the 208-byte run stride puts 16 consecutive runs on 16 distinct bank groups, so
+  // the lanes' 16-byte reads do not conflict; a 192-byte stride repeats every 4 runs),
   // wider teams read them from global memory per token.
   extern __shared__ float4 factor_lds[];
   constexpr bool kLdsFactors = (kKind == kNorm) && kSingle;
@@ -201,7 +204,7 @@ __global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArg
       float m0 = b.x + 1.0f, m1 = b.y + 1.0f, m2 = b.z + 1.0f, m3 = b.w + 1.0f;
       bf16_round2(m0, m1);
       bf16_round2(m2, m3);
-      const int slot = 12 * (c >> 2) + (c & 3);
+      const int slot = kFactorStride * (c >> 2) + (c & 3);
       factor_lds[slot] = make_float4(a.x + 1.0f, a.y + 1.0f, a.z + 1.0f, a.w + 1.0f);
       factor_lds[slot + 4] = make_float4(m0, m1, m2, m3);
       factor_lds[slot + 8] = reinterpret_cast<const float4 *>(args.mod_shift)[c];
@@ -213,9 +216,9 @@ __global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArg
     for (int i = 0; i < 4; ++i) {
       float4 a, b, c;
       if (kLdsFactors) {
-        a = factor_lds[12 * r + i];
-        b = factor_lds[12 * r + 4 + i];
-        c = factor_lds[12 * r + 8 + i];
+        a = factor_lds[kFactorStride * r + i];
+        b = factor_lds[kFactorStride * r + 4 + i];
+        c = factor_lds[kFactorStride * r + 8 + i];
       } else {
         a = reinterpret_cast<const float4 *>(args.norm_scale)[4 * r + i];
         b = reinterpret_cast<const float4 *>(args.mod_scale)[4 * r + i];
@@ -465,7 +468,7 @@ hipError_t launch_team(hipStream_t stream, const PrepareArgs &a) {
   if (per_cu < 1) per_cu = 1;
   const int cap = device_cus() * per_cu;
   dim3 grid(needed < cap ? needed : cap), block(threads);
-  const size_t lds = (kKind == kNorm && kSingle) ? (size_t)a.width * 12 : 0;
+  const size_t lds = (kKind == kNorm && kSingle) ? (size_t)(a.width / 16) * kFactorStride * 16 : 0;
   hipLaunchKernelGGL((prepare_kernel<kKind, T, kSingle>), grid, block, lds, stream, a);
   return hipGetLastError();
 }
