@@ -123,6 +123,10 @@ SHAPES = [
     # the streaming kernel past 32 tokens (short K, grid resident at once): two token
     # groups of 64 and 36
     (100, 1024, 4096, 64),
+    # the largest K (65536): 128 K steps per wave in the few-token kernel; split K over
+    # 128 slices in the tile kernels
+    (3, 65536, 512, 0),
+    (64, 65536, 256, 0),
 ]
 
 
