@@ -394,11 +394,9 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
         else
           wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
+        if (kt + STAGES < kt_count) issue(kt + STAGES);
         read_frags<FM, FN>(af[cur ^ 1], bf[cur ^ 1], smem + ((kt + 1) % STAGES) * kStage,
                            a_row_off, b_row_off, (kh ^ rsw) << 4);
-        // The refill goes out after those reads, so they do not queue behind its LDS
-        // writes (1-3% faster across the large shapes).
-        if (kt + STAGES < kt_count) issue(kt + STAGES);
       }
       if (s + 1 < NS) {
         // The next slice's fragment reads go one between each of the first MFMAs, so
