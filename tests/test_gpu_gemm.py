@@ -169,11 +169,14 @@ def test_rows_past_m_are_never_written():
     assert np.all(host(out)[m:] == 0x5A5A)
 
 
-def test_north_star_shape_checksums_and_sampled_rows():
-    # M=4096, K=3072, N=12288: full-size row and column checksums of the int32
-    # accumulators (size-independent identities) plus exact rows against the oracle.
+@pytest.mark.parametrize("n", [12288, 9216])
+def test_north_star_shape_checksums_and_sampled_rows(n):
+    # M=4096, K=3072 with N=12288 (the north star, 256x256 tiles) and N=9216 (the QKV
+    # GEMM of the bench step, 256x192 tiles): full-size row and column checksums of the
+    # int32 accumulators (size-independent identities) plus exact rows against the
+    # oracle.
     rng = np.random.default_rng(12)
-    m, k, n = 4096, 3072, 12288
+    m, k = 4096, 3072
     a = rng.integers(-127, 128, (m, k), dtype=np.int8)
     w = rng.integers(-127, 128, (n, k), dtype=np.int8)
     A, W = dev(a), dev(w)
