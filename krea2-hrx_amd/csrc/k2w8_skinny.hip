@@ -93,10 +93,21 @@ __global__ __launch_bounds__(WAVES * 64) void stream_kernel(Args g) {
   const int n0 = blockIdx.x * RB;
   const int t0 = blockIdx.y * kTokensPerGroup;
 
+  // SwiGLU over the interleaved 32-row groups [gate o..o+15 | up o..o+15]: with RB=32
+  // a workgroup takes a whole group (rb 0 gates, rb 1 ups); with RB=16 it takes half of
+  // one, 8 gate rows and their 8 up rows (half j = blockIdx.x & 1 of group
+  // blockIdx.x >> 1). Staged rows 0-7 are then the gates, 8-15 the ups, so lanes kq < 2
+  // end with the gates' sums and lanes kq >= 2 with the ups' (exchanged across lane
+  // halves for the epilogue).
+  constexpr bool kPairRows = EPI == kEpiSwiglu && RB == 16;
+  static_assert(EPI != kEpiSwiglu || RB == 16 || RB == 32, "SwiGLU workgroup rows");
+  const int gate0 = 32 * (blockIdx.x >> 1) + 8 * (blockIdx.x & 1), up0 = gate0 + 16;
+
   // Epilogue operands, loaded now. Lane (r, kq) of wave w < TB finishes token
-  // t0 + 16w + r, channels n0 + 16 rb + 4 kq + e (SwiGLU: rb 0 gates, rb 1 ups).
+  // t0 + 16w + r, channels n0 + 16 rb + 4 kq + e (SwiGLU: gate channels gate0 + 4 kq + e
+  // and the matching ups, lanes kq < 2).
   const int tok = t0 + 16 * wave + r;
-  const bool stores = wave < TB && tok < g.m && (AR == 16 || r < 8);
+  const bool stores = wave < TB && tok < g.m && (AR == 16 || r < 8) && (!kPairRows || kq < 2);
   float4 ws[RBK], gs[RBK];
   uint2 prior[RBK], bias[RBK];
   float as = 0.0f;
@@ -105,6 +116,11 @@ __global__ __launch_bounds__(WAVES * 64) void stream_kernel(Args g) {
 #pragma unroll
     for (int rb = 0; rb < RBK; ++rb) {
       const int nb = n0 + 16 * rb + 4 * kq;
+      if (kPairRows) {
+        ws[rb] = *reinterpret_cast<const float4 *>(g.w_scale + gate0 + 4 * kq);
+        gs[rb] = *reinterpret_cast<const float4 *>(g.w_scale + up0 + 4 * kq);
+        continue;
+      }
       if (EPI != kEpiAcc) ws[rb] = *reinterpret_cast<const float4 *>(g.w_scale + nb);
       if (EPI == kEpiResid) {
         gs[rb] = *reinterpret_cast<const float4 *>(g.gate + nb);
@@ -131,7 +147,8 @@ __global__ __launch_bounds__(WAVES * 64) void stream_kernel(Args g) {
     const int c = (lane & 7) ^ skey(row);
     if (i < WL) {
       src[i] = g.w;
-      off[i] = (uint32_t)(n0 + row) * (uint32_t)g.lda + lo * 128 + c * 16;
+      const int wrow = kPairRows ? (i == 0 ? gate0 : up0) + (lane >> 3) : n0 + row;
+      off[i] = (uint32_t)wrow * (uint32_t)g.lda + lo * 128 + c * 16;
     } else {
       src[i] = g.a;
       off[i] = (uint32_t)min(t0 + row, g.m - 1) * (uint32_t)g.lda + lo * 128 + c * 16;
@@ -200,7 +217,7 @@ __global__ __launch_bounds__(WAVES * 64) void stream_kernel(Args g) {
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) partial[((wave * RBK + rb) * TB + tb) * 64 + lane] = acc[rb][tb];
   __syncthreads();
-  if (!stores) return;
+  if (wave >= TB) return;
   v4i sum[RBK];
 #pragma unroll
   for (int rb = 0; rb < RBK; ++rb) {
@@ -208,15 +225,27 @@ __global__ __launch_bounds__(WAVES * 64) void stream_kernel(Args g) {
 #pragma unroll
     for (int w = 1; w < WAVES; ++w) sum[rb] += partial[((w * RBK + rb) * TB + wave) * 64 + lane];
   }
+  v4i pair_up{};
+  if (kPairRows) {
+    // The ups' sums, from lane l + 32 (every lane of the wave takes part in the swap).
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const auto sw = __builtin_amdgcn_permlane32_swap((uint32_t)sum[0][e], (uint32_t)sum[0][e], false, false);
+      pair_up[e] = (int)sw[1];
+    }
+  }
+  if (!stores) return;
   if (EPI == kEpiSwiglu) {
     const float gsv[4] = {ws[0].x, ws[0].y, ws[0].z, ws[0].w};
-    const float usv[4] = {ws[RBK - 1].x, ws[RBK - 1].y, ws[RBK - 1].z, ws[RBK - 1].w};
+    const float4 us = kPairRows ? gs[0] : ws[RBK - 1];
+    const float usv[4] = {us.x, us.y, us.z, us.w};
+    const v4i gate = sum[0], up = kPairRows ? pair_up : sum[RBK - 1];
     uint32_t packed[2];
 #pragma unroll
     for (int e = 0; e < 4; e += 2) {
-      float g0 = ((float)sum[0][e] * gsv[e]) * as, g1 = ((float)sum[0][e + 1] * gsv[e + 1]) * as;
-      float u0 = ((float)sum[RBK - 1][e] * usv[e]) * as;
-      float u1 = ((float)sum[RBK - 1][e + 1] * usv[e + 1]) * as;
+      float g0 = ((float)gate[e] * gsv[e]) * as, g1 = ((float)gate[e + 1] * gsv[e + 1]) * as;
+      float u0 = ((float)up[e] * usv[e]) * as;
+      float u1 = ((float)up[e + 1] * usv[e + 1]) * as;
       bf16_round2(g0, g1);
       bf16_round2(u0, u1);
       float s0 = g0 * sigmoid(g0), s1 = g1 * sigmoid(g1);
@@ -225,7 +254,8 @@ __global__ __launch_bounds__(WAVES * 64) void stream_kernel(Args g) {
       bf16_round2(p0, p1);
       packed[e >> 1] = f16_pack2(p0, p1);
     }
-    uint16_t *out = static_cast<uint16_t *>(g.c) + (int64_t)tok * (g.n >> 1) + (n0 >> 1) + 4 * kq;
+    const int col = kPairRows ? 16 * (blockIdx.x >> 1) + 8 * (blockIdx.x & 1) : n0 >> 1;
+    uint16_t *out = static_cast<uint16_t *>(g.c) + (int64_t)tok * (g.n >> 1) + col + 4 * kq;
     *reinterpret_cast<uint2 *>(out) = make_uint2(packed[0], packed[1]);
     return;
   }
@@ -318,11 +348,17 @@ constexpr int ring_depth_of(int rb, int tb, int ar, int waves) {
   return p < 2 ? 2 : (p > K2W8_SK_PMAX ? K2W8_SK_PMAX : p);
 }
 
-// Workgroup shape: a gate|up pair (32 rows) for SwiGLU, else 16 rows; four waves, or
+// Workgroup shape: 16 rows, or for SwiGLU a whole gate|up group (32 rows) when 16
+// token rows are staged and half of one (8 gates, their 8 ups) when 8 are; four waves, or
 // eight when N/16 workgroups would leave CUs idle (each wave then streams half as
 // many K steps). Measured on the down projection (N=2560, K=9728) against 8-row
 // workgroups of four waves: M=1 7.9 -> 6.8 us, M=16 11.1 -> 8.9, M=32 15.7 -> 11.3.
-int rows_of(int epi) { return epi == kEpiSwiglu ? 32 : 16; }
+// Half groups double the SwiGLU workgroups (N=19456: 608 -> 1216 on 256 CUs), which
+// evens out the last round: up projection at K=2560, M=1 11.3 -> 10.7 us, M=8 11.6 ->
+// 10.8. With 16 token rows each workgroup stages as many token bytes as weight bytes,
+// and twice the workgroups cost more than they even out (M=16 12.3 -> 12.7, M=32 14.0
+// -> 16.2), so there the workgroups keep whole groups.
+int rows_of(int epi, int ar) { return epi == kEpiSwiglu && ar == 16 ? 32 : 16; }
 int waves_of(int epi, int64_t n) { return epi != kEpiSwiglu && n / 16 < device_cus() ? 8 : 4; }
 
 template <int RB, int TB, int AR, int WAVES>
@@ -332,16 +368,18 @@ hipError_t launch_rows(int epi, hipStream_t stream, const Args &a) {
 
 template <int TB, int AR>
 hipError_t launch_tb(int epi, hipStream_t stream, const Args &a) {
-  if (epi == kEpiSwiglu) return launch_rows<32, TB, AR, 4>(epi, stream, a);
+  if constexpr (AR == 16)
+    if (epi == kEpiSwiglu) return launch_rows<32, TB, AR, 4>(epi, stream, a);
   if (waves_of(epi, a.n) == 8) return launch_rows<16, TB, AR, 8>(epi, stream, a);
   return launch_rows<16, TB, AR, 4>(epi, stream, a);
 }
 
 template <int TB, int AR>
 hipError_t set_lds_tb() {
-  hipError_t e = set_lds_stream<32, TB, AR, 4, ring_depth_of(32, TB, AR, 4)>();
-  if (e == hipSuccess) e = set_lds_stream<16, TB, AR, 4, ring_depth_of(16, TB, AR, 4)>();
+  hipError_t e = set_lds_stream<16, TB, AR, 4, ring_depth_of(16, TB, AR, 4)>();
   if (e == hipSuccess) e = set_lds_stream<16, TB, AR, 8, ring_depth_of(16, TB, AR, 8)>();
+  if constexpr (AR == 16)
+    if (e == hipSuccess) e = set_lds_stream<32, TB, AR, 4, ring_depth_of(32, TB, AR, 4)>();
   return e;
 }
 
@@ -355,7 +393,7 @@ bool skinny_streams(int epilogue, const GemmLaunch &l) {
   if (l.m > 128 || l.k > 4096) return false;
   const int64_t tokens = l.m < skinny::kTokensPerGroup ? l.m : skinny::kTokensPerGroup;
   const int tb = (int)((tokens + 15) / 16), ar = tokens <= 8 ? 8 : 16;
-  const int rb = skinny::rows_of(epilogue), waves = skinny::waves_of(epilogue, l.n);
+  const int rb = skinny::rows_of(epilogue, ar), waves = skinny::waves_of(epilogue, l.n);
   const int lds_kb = waves * skinny::ring_depth_of(rb, tb, ar, waves) * (rb / 8 + tb * ar / 8);
   const int64_t per_cu = 160 / lds_kb;
   const int64_t grid = (l.n / rb) * ((l.m + skinny::kTokensPerGroup - 1) / skinny::kTokensPerGroup);
@@ -385,9 +423,7 @@ hipError_t launch_skinny(int epilogue, hipStream_t stream, const GemmLaunch &l) 
   a.k = (int)l.k;
   a.lda = (int)l.lda;
   const int tokens = (int)(l.m < skinny::kTokensPerGroup ? l.m : skinny::kTokensPerGroup);
-#ifndef K2W8_SK_NO_A8
   if (tokens <= 8) return skinny::launch_tb<1, 8>(epilogue, stream, a);
-#endif
   switch ((tokens + 15) / 16) {
     case 1: return skinny::launch_tb<1, 16>(epilogue, stream, a);
     case 2: return skinny::launch_tb<2, 16>(epilogue, stream, a);

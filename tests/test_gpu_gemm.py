@@ -216,12 +216,14 @@ def test_convrot_known_answer_through_prepare_and_gemm(inputs):
     assert np.array_equal(host(out), want)
 
 
-def test_swiglu_reads_the_sixteen_row_interleave():
+@pytest.mark.parametrize("m", [64, 5])
+def test_swiglu_reads_the_sixteen_row_interleave(m):
     # Gate rows of group j are rows 32j..32j+15 and up rows 32j+16..32j+31
     # (src/checkpoint/plan.rs:193-208): permuting the interleave must change the output
-    # exactly as the oracle says.
+    # exactly as the oracle says. m=5 runs the few-token kernel, whose workgroups each
+    # take half a group (8 gate rows and their 8 up rows).
     rng = np.random.default_rng(13)
-    m, k, n = 64, 256, 256
+    k, n = 256, 256
     a = int8_weights(rng, m, k)
     w = int8_weights(rng, n, k)
     ws = channel_scales(rng, n)
