@@ -421,7 +421,7 @@ __global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArg
         v4u out;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          uint32_t word = 0;
+          uint32_t biased[4];
 #pragma unroll
           for (int b = 0; b < 4; ++b) {
             // clamp(rne(x), +-127) == rne(clamp(x, +-127)) as the bounds are integers
@@ -430,10 +430,11 @@ __global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArg
             float qv = v[t][4 * i + b] * inv;
             qv = fmaxf(qv, -127.0f);
             qv = fminf(qv, 127.0f);
-            const float biased = qv + 12582912.0f;
-            word |= (__float_as_uint(biased) & 0xffu) << (8 * b);
+            biased[b] = __float_as_uint(qv + 12582912.0f);
           }
-          out[i] = word;
+          // Low bytes of the four words, in order (v_perm selector 0x0c gives 0).
+          out[i] = __builtin_amdgcn_perm(biased[1], biased[0], 0x0c0c0400u) |
+                   __builtin_amdgcn_perm(biased[3], biased[2], 0x04000c0cu);
         }
         *reinterpret_cast<v4u *>(qr + ((run0 + 64 * t) << 4)) = out;
       }
