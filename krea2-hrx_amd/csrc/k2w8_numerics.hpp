@@ -35,11 +35,18 @@ __device__ __forceinline__ uint32_t bf16_pack2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(k2w8_f2{a, b}, k2w8_bf2));
 }
 
-// Two values rounded to bf16 and widened back to f32 (bf16_round on each).
+// One value rounded to bf16 and widened back to f32 (bf16_round), in one hardware
+// conversion: packing (0, x) puts bf16(x) in the high half over a zero low half, which
+// is the widened value itself.
+__device__ __forceinline__ float bf16_round1(float x) {
+  return __builtin_bit_cast(float, __builtin_convertvector(k2w8_f2{0.0f, x}, k2w8_bf2));
+}
+
+// Two values rounded to bf16 and widened back to f32 (bf16_round on each): two
+// conversions, against one conversion of the pair and two instructions to unpack it.
 __device__ __forceinline__ void bf16_round2(float &a, float &b) {
-  const uint32_t u = bf16_pack2(a, b);
-  a = __uint_as_float(u << 16);
-  b = __uint_as_float(u & 0xffff0000u);
+  a = bf16_round1(a);
+  b = bf16_round1(b);
 }
 
 // Two f32 values to packed f16 (low half first), round to nearest even.
