@@ -456,16 +456,24 @@ __global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArg
 }
 
 // Waves per CU the persistent grid aims for: enough to cover load latency while each
-// team still loops over several tokens.
+// team still loops over several tokens. The norm prepare's one-wave teams do better
+// with fewer, longer-lived waves, whose prefetch of the next row overlaps the current
+// row's compute (a round of one row per wave loads everything, then computes): with
+// cold rows, M=4544 20.6 -> 19.5 us, width 4096 24.6 -> 23.3 us. The gated prepare
+// loses a third at 8 (24.4 -> 35.0 us).
 #ifndef K2W8_PREPARE_WAVES_PER_CU
 #define K2W8_PREPARE_WAVES_PER_CU 32
+#endif
+#ifndef K2W8_PREPARE_NORM_WAVES_PER_CU
+#define K2W8_PREPARE_NORM_WAVES_PER_CU 8
 #endif
 
 template <int kKind, int T, bool kSingle>
 hipError_t launch_team(hipStream_t stream, const PrepareArgs &a) {
   const int threads = 64 * a.wpt * a.teams;
   const int needed = (a.tokens + a.teams - 1) / a.teams;
-  int per_cu = K2W8_PREPARE_WAVES_PER_CU / (a.wpt * a.teams);
+  const int waves = (kKind == kNorm && kSingle) ? K2W8_PREPARE_NORM_WAVES_PER_CU : K2W8_PREPARE_WAVES_PER_CU;
+  int per_cu = waves / (a.wpt * a.teams);
   if (per_cu < 1) per_cu = 1;
   const int cap = device_cus() * per_cu;
   dim3 grid(needed < cap ? needed : cap), block(threads);
