@@ -100,6 +100,10 @@ int k2w8_prepare_plain_i8(void *stream, const k2w8_prepare_plain_cfg *cfg, int64
  * bound by Session::block (src/session/mod.rs:757-770).
  *   attn f16 [tokens][width], gate f16 [tokens][gate_stride]
  *   -> q int8 [tokens][out_stride], q_scale f32 [tokens]
+ * The first call on a device builds the device's 128 KiB table of bf16(sigmoid(g))
+ * over all f16 gates (a static device array) on `stream` and synchronises `stream`
+ * once; that first call must not be inside a stream capture (k2w8_blocks_record sets
+ * the device up before it captures).
  */
 int k2w8_prepare_gated_i8(void *stream, const k2w8_prepare_gated_cfg *cfg, int64_t tokens,
                           const void *attn, const void *gate, int8_t *q, float *q_scale);

@@ -147,6 +147,8 @@ int k2w8_prime_launches(void *stream) {
   // Allocate the stream's split-K workspace now, outside the capture, so recorded
   // GEMMs may split K as eager ones do.
   (void)k2w8::splitk_workspace(static_cast<hipStream_t>(stream));
+  const hipError_t e = k2w8::prepare_gated_ready(static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return runtime("blocks_record: the gated prepare's sigmoid table", e);
   return K2W8_OK;
 }
 
@@ -215,6 +217,11 @@ int k2w8_prepare_gated_i8(void *stream, const k2w8_prepare_gated_cfg *cfg, int64
                 (long long)cfg->gate_stride);
   if (!aligned(gate, 16)) return fail(K2W8_INVALID_ARGUMENT, "%s: gate must be 16-byte aligned", stage);
   if ((rc = ensure_configured(stage)) != K2W8_OK) return rc;
+  hipError_t e = k2w8::prepare_gated_ready(static_cast<hipStream_t>(stream));
+  if (e == hipErrorStreamCaptureUnsupported)
+    return fail(K2W8_RUNTIME, "%s: the first call on a device must not be inside a stream capture "
+                "(k2w8_prime_launches sets the device up beforehand)", stage);
+  if (e != hipSuccess) return runtime(stage, e);
   k2w8::PrepareLaunch p;
   p.h = attn;
   p.gate = gate;
@@ -223,7 +230,7 @@ int k2w8_prepare_gated_i8(void *stream, const k2w8_prepare_gated_cfg *cfg, int64
   p.width = cfg->width;
   p.out_stride = cfg->out_stride;
   p.gate_stride = cfg->gate_stride;
-  hipError_t e = k2w8::launch_prepare(2, static_cast<hipStream_t>(stream), tokens, p);
+  e = k2w8::launch_prepare(2, static_cast<hipStream_t>(stream), tokens, p);
   if (e != hipSuccess) return runtime(stage, e);
   return ok();
 }

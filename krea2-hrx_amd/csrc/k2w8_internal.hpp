@@ -19,6 +19,9 @@ struct PrepareLaunch {
 // kind: 0 norm, 1 plain, 2 gated
 hipError_t launch_prepare(int kind, hipStream_t stream, int64_t tokens, const PrepareLaunch &p);
 hipError_t configure_prepare_lds();
+// One-time set-up of the gated prepare on the current device (its sigmoid table); not
+// inside a stream capture.
+hipError_t prepare_gated_ready(hipStream_t stream);
 
 enum Epilogue { kEpiPlain = 0, kEpiResid = 1, kEpiSwiglu = 2, kEpiBias = 3, kEpiAcc = 4 };
 

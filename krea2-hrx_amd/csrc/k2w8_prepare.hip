@@ -34,6 +34,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "k2w8_numerics.hpp"
 #include "k2w8_internal.hpp"
 
@@ -124,6 +126,21 @@ struct PrepareArgs {
 };
 
 // Raw input of one lane for one token: T runs of 16 f16/bf16 (and the gate's).
+// bf16(sigmoid(g)) for every f16 bit pattern g, as bf16 bits: the gated prepare's
+// gate factor (kernels/prepare_gated_i8.loom:97-101) depends on the 16 bits of the gate
+// alone. Filled once per device by `sigmoid_table_kernel` from the same device
+// functions the formula uses, so a lookup gives the formula's bits. A gated block
+// copies it into LDS (128 KiB) and looks each gate up there.
+__device__ __align__(16) uint16_t g_sigmoid_bf16[65536];
+constexpr size_t kSigmoidTableBytes = sizeof(uint16_t) * 65536;
+constexpr int kGatedWaves = 16;  // waves per gated block: one block per CU (the table)
+
+__global__ __launch_bounds__(256) void sigmoid_table_kernel() {
+  const int b = blockIdx.x * 256 + threadIdx.x;
+  const float s = bf16_round1(sigmoid(f16_value((uint16_t)b)));
+  g_sigmoid_bf16[b] = (uint16_t)(__float_as_uint(s) >> 16);
+}
+
 template <int kKind, int T>
 struct Raw {
   v4u x[T][2];
@@ -132,7 +149,7 @@ struct Raw {
 
 constexpr int kMaxThreads = 1024;
 constexpr int kFactorStride = 13;  // float4 slots per run of staged norm factors
-constexpr int kMaxTeams = 4;
+constexpr int kMaxTeams = 16;  // teams per block (single-wave teams, or gated teams)
 constexpr int kMaxWpt = 16;
 
 // Threads per block a kernel is compiled for: teams of up to 16 waves hold one or two
@@ -197,6 +214,13 @@ __global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArg
   // wider teams read them from global memory per token.
   extern __shared__ float4 factor_lds[];
   constexpr bool kLdsFactors = (kKind == kNorm) && kSingle;
+  if (kKind == kGated) {
+    const uint4 *src = reinterpret_cast<const uint4 *>(g_sigmoid_bf16);
+    for (int c = threadIdx.x; c < (int)(kSigmoidTableBytes / 16); c += blockDim.x)
+      reinterpret_cast<uint4 *>(factor_lds)[c] = src[c];
+    __syncthreads();
+  }
+  const uint16_t *sigmoid_lds = reinterpret_cast<const uint16_t *>(factor_lds);
   if (kLdsFactors) {
     for (int c = threadIdx.x; c < (width >> 2); c += blockDim.x) {
       const float4 a = reinterpret_cast<const float4 *>(args.norm_scale)[c];
@@ -381,9 +405,9 @@ __global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArg
           const uint32_t gw = cur.g[t][i >> 3][(i >> 1) & 3];
           float a0 = f16_value((uint16_t)(aw & 0xffffu)), a1 = f16_value((uint16_t)(aw >> 16));
           bf16_round2(a0, a1);
-          float s0 = sigmoid(f16_value((uint16_t)(gw & 0xffffu)));
-          float s1 = sigmoid(f16_value((uint16_t)(gw >> 16)));
-          bf16_round2(s0, s1);
+          // bf16(sigmoid(g)) from the table (the formula's bits).
+          const float s0 = bf16_value(sigmoid_lds[gw & 0xffffu]);
+          const float s1 = bf16_value(sigmoid_lds[gw >> 16]);
           float p0 = a0 * s0, p1 = a1 * s1;
           bf16_round2(p0, p1);
           v[t][i] = p0;
@@ -472,12 +496,16 @@ template <int kKind, int T, bool kSingle>
 hipError_t launch_team(hipStream_t stream, const PrepareArgs &a) {
   const int threads = 64 * a.wpt * a.teams;
   const int needed = (a.tokens + a.teams - 1) / a.teams;
-  const int waves = (kKind == kNorm && kSingle) ? K2W8_PREPARE_NORM_WAVES_PER_CU : K2W8_PREPARE_WAVES_PER_CU;
+  const int waves = (kKind == kNorm && kSingle) ? K2W8_PREPARE_NORM_WAVES_PER_CU
+                    : kKind == kGated            ? kGatedWaves
+                                                 : K2W8_PREPARE_WAVES_PER_CU;
   int per_cu = waves / (a.wpt * a.teams);
   if (per_cu < 1) per_cu = 1;
   const int cap = device_cus() * per_cu;
   dim3 grid(needed < cap ? needed : cap), block(threads);
-  const size_t lds = (kKind == kNorm && kSingle) ? (size_t)(a.width / 16) * kFactorStride * 16 : 0;
+  const size_t lds = (kKind == kNorm && kSingle) ? (size_t)(a.width / 16) * kFactorStride * 16
+                     : kKind == kGated            ? kSigmoidTableBytes
+                                                  : 0;
   hipLaunchKernelGGL((prepare_kernel<kKind, T, kSingle>), grid, block, lds, stream, a);
   return hipGetLastError();
 }
@@ -489,7 +517,7 @@ hipError_t launch_team(hipStream_t stream, const PrepareArgs &a) {
 // Team shape for a row: the fewest waves (at most 16) that hold it with at most
 // `max_runs` runs of 16 elements per lane; single-wave teams are packed four to a
 // block and two-wave teams two to a block.
-void team_shape(PrepareArgs &a, int max_runs, int &t) {
+void team_shape(PrepareArgs &a, int max_runs, bool gated, int &t) {
   const int runs = a.width >> 4;
   int wpt = (runs + 64 * max_runs - 1) / (64 * max_runs);
   if (wpt > kMaxWpt) wpt = kMaxWpt;
@@ -499,7 +527,10 @@ void team_shape(PrepareArgs &a, int max_runs, int &t) {
     wpt = (runs + 127) / 128;
   }
   a.wpt = wpt;
-  a.teams = wpt == 1 ? kMaxTeams : (wpt == 2 ? 2 : 1);
+  a.teams = wpt == 1 ? 4 : (wpt == 2 ? 2 : 1);
+  // A gated block holds the sigmoid table in LDS: one block per CU, as many teams as
+  // fit 16 waves.
+  if (gated) a.teams = kGatedWaves / wpt;
 }
 
 template <int kKind, bool kSingle>
@@ -520,7 +551,7 @@ hipError_t launch_kind(hipStream_t stream, PrepareArgs a) {
   // one (more waves per row: its sigmoid makes each element dearer).
   constexpr int kRuns = kKind == kNorm ? 4 : (kKind == kPlain ? 3 : K2W8_PREPARE_MAX_RUNS_PER_LANE);
   int t = 1;
-  team_shape(a, kRuns, t);
+  team_shape(a, kRuns, kKind == kGated, t);
   if (a.wpt == 1) return launch_t<kKind, true>(t, stream, a);
   return launch_t<kKind, false>(t, stream, a);
 }
@@ -549,6 +580,46 @@ hipError_t launch_prepare(int kind, hipStream_t stream, int64_t tokens, const Pr
 }
 
 // The prepares use static LDS only.
-hipError_t configure_prepare_lds() { return hipSuccess; }
+hipError_t configure_prepare_lds() {
+  // The gated prepare's sigmoid table (128 KiB of dynamic LDS).
+  const void *fns[8] = {reinterpret_cast<const void *>(prepare_kernel<kGated, 1, true>),
+                        reinterpret_cast<const void *>(prepare_kernel<kGated, 2, true>),
+                        reinterpret_cast<const void *>(prepare_kernel<kGated, 3, true>),
+                        reinterpret_cast<const void *>(prepare_kernel<kGated, 4, true>),
+                        reinterpret_cast<const void *>(prepare_kernel<kGated, 1, false>),
+                        reinterpret_cast<const void *>(prepare_kernel<kGated, 2, false>),
+                        reinterpret_cast<const void *>(prepare_kernel<kGated, 3, false>),
+                        reinterpret_cast<const void *>(prepare_kernel<kGated, 4, false>)};
+  for (const void *f : fns) {
+    const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kSigmoidTableBytes);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+// The sigmoid table of the current device, filled on its first use there: on `stream`,
+// which is then synchronised, so that calls on any stream of the device find it
+// complete. A stream capture cannot run it (the fill would only be recorded), so the
+// first use on a device must come before any capture; k2w8_prime_launches does it.
+hipError_t prepare_gated_ready(hipStream_t stream) {
+  static std::mutex mu;
+  constexpr int kMaxDevices = 64;
+  static bool ready[kMaxDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (ready[dev]) return hipSuccess;
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  e = hipStreamIsCapturing(stream, &capture);
+  if (e != hipSuccess) return e;
+  if (capture != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
+  hipLaunchKernelGGL(sigmoid_table_kernel, dim3(256), dim3(256), 0, stream);
+  e = hipGetLastError();
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  if (e == hipSuccess) ready[dev] = true;
+  return e;
+}
 
 }  // namespace k2w8

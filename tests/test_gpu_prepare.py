@@ -132,6 +132,22 @@ def test_gated_prepare_is_bit_exact_with_the_oracle(width):
     assert_same(q, s, q_ref, s_ref, width)
 
 
+def test_gated_prepare_over_every_gate_value():
+    # The gate factor bf16(sigmoid(g)) comes from a table indexed by the gate's 16 bits:
+    # rows holding every f16 pattern (NaNs replaced by 0), shuffled, with attn values
+    # near 1 so that each product keeps the factor's magnitude.
+    rng = np.random.default_rng(77)
+    tokens, width = 16, 4096
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    nan = np.isnan(bits.view(np.float16))
+    bits[nan] = 0
+    gb = rng.permutation(bits).reshape(tokens, width)
+    a = f16_bits(rng.uniform(0.5, 1.5, (tokens, width)).astype(np.float32))
+    q, s = run_gated(a, gb, tokens, width, width, width)
+    q_ref, s_ref = oracle.prepare_gated(a, gb, width, width, width)
+    assert_same(q, s, q_ref, s_ref, width)
+
+
 @pytest.mark.parametrize("kind", ["norm", "plain", "gated"])
 def test_prepares_are_bit_exact_at_the_baseline_shape(kind):
     # M=4096 (and 4544) tokens of width 3072.

@@ -43,6 +43,9 @@ def inputs() -> np.ndarray:
         band(-0.01, -0.02), band(0.01, 0.02),
         np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-45, -1e-45, 3.4028235e38,
                   -3.4028235e38], np.float32),
+        # every f16 value: the gated prepare looks bf16(sigmoid(g)) up in a table built
+        # from this function for each of them
+        np.arange(1 << 16, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32),
     ]
     return np.concatenate(parts)
 
