@@ -86,6 +86,30 @@ __device__ __forceinline__ void radix4_reg(float (&v)[16]) {
   }
 }
 
+// The same stage on f16 values, for the plain prepare, whose every stage ends in
+// f16(0.25 * o): the first sums e0 + e1, e0 - e1, ... read the f16 halves directly
+// (v_fma_mix_f32: fma(e0, one, +-e1) is the f32 sum or difference of the widened
+// values, rounded once), so no widening instruction precedes the stage. `one` is 1.0
+// from a register: with a literal the compiler folds the fma into a widening and an add.
+template <int S>
+__device__ __forceinline__ void radix4_reg_f16(_Float16 (&v)[16], float one) {
+#pragma unroll
+  for (int block = 0; block < 16; block += 4 * S) {
+#pragma unroll
+    for (int c = 0; c < S; ++c) {
+      const int i = block + c;
+      const float s01 = __builtin_fmaf((float)v[i], one, (float)v[i + S]);
+      const float d01 = __builtin_fmaf((float)v[i], one, -(float)v[i + S]);
+      const float s23 = __builtin_fmaf((float)v[i + 2 * S], one, (float)v[i + 3 * S]);
+      const float d23 = __builtin_fmaf((float)v[i + 2 * S], one, -(float)v[i + 3 * S]);
+      v[i] = (_Float16)((s01 + d23) * 0.25f);
+      v[i + S] = (_Float16)((s01 - d23) * 0.25f);
+      v[i + 2 * S] = (_Float16)((d01 + s23) * 0.25f);
+      v[i + 3 * S] = (_Float16)((s23 - d01) * 0.25f);
+    }
+  }
+}
+
 // Stride-16 stage: e0..e3 sit in lanes q = 0..3 of a quad (element bits 4, 5 = lane
 // bits 0, 1). S = own + partner(xor 1) is s01 or s23; D = partner - own is -d01, d01,
 // -d23, d23 for q = 0..3; o_q = S - D(q xor 2).
@@ -123,6 +147,7 @@ struct PrepareArgs {
   float eps;
   int wpt;    // waves per token team
   int teams;  // teams per block
+  float one;  // 1.0 (see radix4_reg_f16)
 };
 
 // Raw input of one lane for one token: T runs of 16 f16/bf16 (and the gate's).
@@ -390,13 +415,18 @@ __global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArg
           v[t][i + 1] = c1;
         }
       } else if (kKind == kPlain) {
-        // kernels/prepare_plain_i8.loom:89-90
+        // kernels/prepare_plain_i8.loom:89-90; stages 1 and 4 on the f16 values.
+        _Float16 hv[16];
 #pragma unroll
         for (int i = 0; i < 16; i += 2) {
           const uint32_t word = cur.x[t][i >> 3][(i >> 1) & 3];
-          v[t][i] = f16_value((uint16_t)(word & 0xffffu));
-          v[t][i + 1] = f16_value((uint16_t)(word >> 16));
+          hv[i] = __builtin_bit_cast(_Float16, (uint16_t)(word & 0xffffu));
+          hv[i + 1] = __builtin_bit_cast(_Float16, (uint16_t)(word >> 16));
         }
+        radix4_reg_f16<1>(hv, args.one);
+        radix4_reg_f16<4>(hv, args.one);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[t][i] = (float)hv[i];
       } else {
         // kernels/prepare_gated_i8.loom:86-108
 #pragma unroll
@@ -414,8 +444,10 @@ __global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArg
           v[t][i + 1] = p1;
         }
       }
-      radix4_reg<1, kQuarter>(v[t]);
-      radix4_reg<4, kQuarter>(v[t]);
+      if (kKind != kPlain) {
+        radix4_reg<1, kQuarter>(v[t]);
+        radix4_reg<4, kQuarter>(v[t]);
+      }
       radix4_quad<kQuarter>(v[t]);
       radix4_row<kQuarter>(v[t]);
 #pragma unroll
@@ -572,6 +604,7 @@ hipError_t launch_prepare(int kind, hipStream_t stream, int64_t tokens, const Pr
   a.out_stride = (int)p.out_stride;
   a.gate_stride = (int)p.gate_stride;
   a.eps = p.eps;
+  a.one = 1.0f;
   switch (kind) {
     case kNorm: return launch_kind<kNorm>(stream, a);
     case kPlain: return launch_kind<kPlain>(stream, a);
