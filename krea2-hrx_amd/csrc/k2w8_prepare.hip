@@ -150,7 +150,6 @@ struct PrepareArgs {
   float one;  // 1.0 (see radix4_reg_f16)
 };
 
-// Raw input of one lane for one token: T runs of 16 f16/bf16 (and the gate's).
 // bf16(sigmoid(g)) for every f16 bit pattern g, as bf16 bits: the gated prepare's
 // gate factor (kernels/prepare_gated_i8.loom:97-101) depends on the 16 bits of the gate
 // alone. Filled once per device by `sigmoid_table_kernel` from the same device
@@ -166,6 +165,7 @@ __global__ __launch_bounds__(256) void sigmoid_table_kernel() {
   g_sigmoid_bf16[b] = (uint16_t)(__float_as_uint(s) >> 16);
 }
 
+// Raw input of one lane for one token: T runs of 16 f16/bf16 (and the gate's).
 template <int kKind, int T>
 struct Raw {
   v4u x[T][2];
@@ -174,7 +174,7 @@ struct Raw {
 
 constexpr int kMaxThreads = 1024;
 constexpr int kFactorStride = 13;  // float4 slots per run of staged norm factors
-constexpr int kMaxTeams = 16;  // teams per block (single-wave teams, or gated teams)
+constexpr int kMaxTeams = 16;  // most teams in a block (gated blocks pack up to 16)
 constexpr int kMaxWpt = 16;
 
 // Threads per block a kernel is compiled for: teams of up to 16 waves hold one or two
