@@ -210,3 +210,71 @@ def test_quantiser_scale_is_amax_over_127_and_codes_saturate():
     q, s = oracle.prepare_plain(z.view(np.uint16), 512, 512)
     assert np.all(q == 0)
     assert np.all(s == np.float32(np.float32(1e-30) / np.float32(127.0)))
+
+
+def _bias_case(seed, m=37, n=96, k=256):
+    rng = np.random.default_rng(seed)
+    a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    ws = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    s = rng.uniform(1e-3, 5e-2, m).astype(np.float32)
+    bias = (rng.standard_normal(n) * 0.02).astype(np.float16)
+    acc = a.astype(np.int64) @ w.astype(np.int64).T  # brute-force dot, not the oracle's
+    return acc.astype(np.int32), ws, s, bias
+
+
+def test_bias_epilogue_with_a_zero_bias_is_the_plain_epilogue():
+    # The bias epilogue adds one f32 term before the bf16 rounding: with a -0.0 bias
+    # (x + -0 == x for every x, +0 included) it must equal the plain epilogue bit for bit,
+    # whose formula the reference's ConvRot known answer pins.
+    acc, ws, s, bias = _bias_case(11)
+    neg_zero = np.full(bias.shape, 0x8000, np.uint16)
+    assert np.array_equal(oracle.epilogue_bias(acc, ws, s, neg_zero),
+                          oracle.epilogue_plain(acc, ws, s))
+    pos_zero = np.zeros(bias.shape, np.uint16)
+    assert np.array_equal(oracle.epilogue_bias(acc, ws, s, pos_zero),
+                          oracle.epilogue_plain(acc, ws, s))
+
+
+def test_bias_epilogue_of_a_zero_accumulator_is_the_rounded_bias():
+    # acc = 0 leaves exactly the bias: out = f16(bf16(bias)), with bf16 rounding by torch
+    # and f16 by numpy (independent of the oracle's conversions).
+    _, ws, s, bias = _bias_case(12)
+    acc = np.zeros((s.size, ws.size), np.int32)
+    out = oracle.epilogue_bias(acc, ws, s, bias.view(np.uint16))
+    want = torch.from_numpy(bias.astype(np.float32)).to(torch.bfloat16).float().numpy()
+    want = np.broadcast_to(want.astype(np.float16).view(np.uint16), out.shape)
+    assert np.array_equal(out, want)
+
+
+def test_bias_epilogue_is_within_one_bf16_ulp_of_the_exact_value():
+    # Closed form in f64: v = acc * ws * as + bias. The f32 evaluation rounds twice before
+    # the bf16 rounding, so the stored value is within one bf16 ulp of bf16(v) (and the
+    # store is on the bf16 grid); a dropped or mis-signed bias term is off by far more.
+    acc, ws, s, bias = _bias_case(13)
+    out = oracle.epilogue_bias(acc, ws, s, bias.view(np.uint16)).view(np.float16).astype(np.float64)
+    v = acc.astype(np.float64) * ws.astype(np.float64)[None, :] * s.astype(np.float64)[:, None]
+    v += bias.astype(np.float64)[None, :]
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(v), 2.0 ** -30))) - 7)
+    # three f32 roundings before the bf16 one: each within 2^-24 of its operands' size
+    f32_err = 4 * 2.0 ** -24 * (np.abs(v - bias.astype(np.float64)[None, :]) +
+                                np.abs(bias.astype(np.float64))[None, :])
+    assert np.all(np.abs(out - v) <= ulp + f32_err)
+    assert np.array_equal(bf16_value(oracle.bf16_bits(out.astype(np.float32))), out.astype(np.float32))
+    # the bias matters at this scale: dropping it moves many outputs by more than an ulp
+    no_bias = v - bias.astype(np.float64)[None, :]
+    assert (np.abs(out - no_bias) > 2 * ulp).mean() > 0.1
+
+
+def test_fused_cpu_gemm_is_the_integer_gemm_then_the_plain_epilogue():
+    # ora_gemm_i8 (the fused CPU baseline) against the separately pinned parts, at a
+    # padded row stride and a ragged token count.
+    rng = np.random.default_rng(14)
+    m, n, k, stride = 45, 160, 384, 448
+    a = rng.integers(-127, 128, (m, stride), dtype=np.int8)
+    w = rng.integers(-127, 128, (n, stride), dtype=np.int8)
+    ws = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    s = rng.uniform(1e-3, 5e-2, m).astype(np.float32)
+    want = oracle.epilogue_plain(oracle.gemm_i32(a, w, m, n, k, stride), ws, s)
+    for threads in (1, 0):
+        assert np.array_equal(oracle.gemm_i8(a, w, m, n, k, stride, ws, s, threads=threads), want)
