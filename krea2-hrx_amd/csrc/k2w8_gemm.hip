@@ -387,8 +387,13 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
       if (s + 1 < NS) {
         read_frags<FM, FN>(af[cur ^ 1], bf[cur ^ 1], stage, a_row_off, b_row_off,
                            ((2 * (s + 1) + kh) ^ rsw) << 4);
-      } else if (kt + 1 < kt_count) {
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      } else {
+        // lgkmcnt(0), through the builtin so that the compiler's own wait insertion
+        // sees it on every path into the last slice (else it waits there for the next
+        // stage's first fragment reads before the slice's first MFMAs).
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+      }
+      if (s + 1 == NS && kt + 1 < kt_count) {
         if (kt + STAGES - 1 < kt_count)
           wait_vmcnt<(STAGES - 2) * kIns>();
         else
