@@ -4,12 +4,14 @@
  * One entry point per reference kernel, with the reference's positional buffer
  * bindings in the reference's order, its compile-time configuration passed as a
  * struct (one field per `config.decl`), and its one runtime scalar (`tokens` or
- * `m_size`). Every pointer is device memory the caller owns. The library allocates
- * one thing itself: GEMMs whose output tiles would leave most CUs idle split K, and
- * their int32 partial sums go to a 64 MiB workspace per (device, stream), allocated
- * on the first such call outside a stream capture and kept until the process ends
- * (under capture, without it, the call runs unsplit). `stream` is a hipStream_t
- * (NULL: the null stream). Calls enqueue work and return; they do not synchronise.
+ * `m_size`). Every pointer is device memory the caller owns. GEMMs whose output
+ * tiles would leave most CUs idle split K and keep int32 partial sums in a split-K
+ * workspace: the caller's, registered per stream with k2w8_gemm_set_workspace, or else
+ * one the library allocates per (device, stream) on the first such call outside a
+ * stream capture (k2w8_gemm_workspace_bytes() bytes, kept until the process ends; under
+ * capture, without either, the call runs unsplit). A recorded block graph owns its own
+ * workspace. `stream` is a hipStream_t (NULL: the null stream). Calls enqueue work and
+ * return; they do not synchronise.
  *
  * Data types on the buffers:
  *   f16 / bf16 activations: 16-bit IEEE half / bfloat16 bit patterns
@@ -35,7 +37,7 @@ extern "C" {
 #define K2W8_RUNTIME (-3)          /* Error::Runtime (a hipError_t) */
 
 /* The ABI revision this header describes. */
-#define K2W8_ABI_VERSION 2
+#define K2W8_ABI_VERSION 3
 int k2w8_abi_version(void);
 
 /* Message of the last failure on the calling thread ("" after success). */
@@ -165,6 +167,25 @@ int k2w8_gemm_i8_bias(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, const i
  */
 int k2w8_gemm_i8_acc(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, const int8_t *a,
                      const int8_t *w, int32_t *acc);
+
+/*
+ * Split-K workspace of a stream. Replaces the session-owned GEMM workspaces of
+ * src/session/mod.rs:321-340 (the reference's session allocates every buffer up front
+ * and its launches allocate nothing).
+ *
+ * gemm_set_workspace: GEMM calls on `stream` (current device) keep their split-K
+ * partial sums in `workspace` (`bytes` of device memory, 256-byte aligned, >= 256)
+ * instead of a library allocation, so they never allocate, also under stream capture
+ * (a captured split-K GEMM then splits as an eager one does). The number of K slices is
+ * capped by what fits: a smaller workspace means fewer slices, never a failure. The
+ * caller keeps the memory alive while it is registered and while work already enqueued
+ * may use it; calls on one stream are ordered, so they may share it. A null workspace
+ * removes the registration (the library's own buffer is used again).
+ * gemm_workspace_bytes: the size of the library's own per-stream workspace, which
+ * holds every split this build chooses.
+ */
+int k2w8_gemm_set_workspace(void *stream, void *workspace, int64_t bytes);
+int64_t k2w8_gemm_workspace_bytes(void);
 
 /*
  * lora_transport: replaces krea2_lora_transport (kernels/native/lora_transport.loom:5-41),

@@ -144,9 +144,6 @@ int k2w8_prime_launches(void *stream) {
   int rc = ensure_configured("blocks_record");
   if (rc != K2W8_OK) return rc;
   (void)k2w8::device_cus();
-  // Allocate the stream's split-K workspace now, outside the capture, so recorded
-  // GEMMs may split K as eager ones do.
-  (void)k2w8::splitk_workspace(static_cast<hipStream_t>(stream));
   const hipError_t e = k2w8::prepare_gated_ready(static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return runtime("blocks_record: the gated prepare's sigmoid table", e);
   return K2W8_OK;
@@ -267,6 +264,19 @@ int k2w8_gemm_i8_bias(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, const i
   return run_gemm("gemm_i8_bias", k2w8::kEpiBias, stream, cfg, m, a, w, scale, a_scale, c,
                   nullptr, bias);
 }
+
+int k2w8_gemm_set_workspace(void *stream, void *workspace, int64_t bytes) {
+  if (workspace && (bytes < 256 || !aligned(workspace, 256)))
+    return fail(K2W8_INVALID_ARGUMENT,
+                "gemm_set_workspace: workspace must be 256-byte aligned and at least 256 bytes, "
+                "got %lld bytes", (long long)bytes);
+  hipError_t e = k2w8::splitk_register(static_cast<hipStream_t>(stream), workspace,
+                                       workspace ? (size_t)bytes : 0);
+  if (e != hipSuccess) return runtime("gemm_set_workspace", e);
+  return ok();
+}
+
+int64_t k2w8_gemm_workspace_bytes(void) { return (int64_t)k2w8::splitk_workspace_bytes(); }
 
 int k2w8_gemm_i8_acc(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, const int8_t *a,
                      const int8_t *w, int32_t *acc) {

@@ -18,6 +18,7 @@
 #include <vector>
 
 #include "krea2_w8a8.h"
+#include "k2w8_internal.hpp"
 
 int k2w8_fail_invalid(const char *message);
 int k2w8_fail_runtime(const char *stage, hipError_t e);
@@ -246,9 +247,13 @@ const Stage &stage_at(int64_t k) {
 struct k2w8_graph {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
+  // The split-K workspace the recorded GEMMs write: the graph's own, so a replay on
+  // any stream never shares partial sums with eager calls on the recording stream.
+  void *workspace = nullptr;
   ~k2w8_graph() {
     if (exec) (void)hipGraphExecDestroy(exec);
     if (graph) (void)hipGraphDestroy(graph);
+    if (workspace) (void)hipFree(workspace);
   }
 };
 
@@ -295,10 +300,15 @@ int k2w8_blocks_record(void *stream, const k2w8_block_cfg *cfg, int64_t layers,
   int rc = k2w8_prime_launches(stream);
   if (rc != K2W8_OK) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
-  if (e != hipSuccess) return k2w8_fail_runtime(stage, e);
-  for (int64_t i = 0; i < layers && rc == K2W8_OK; ++i) rc = run_block(stream, cfg, i, weights + i, buffers);
   auto g = std::make_unique<k2w8_graph>();
+  const size_t ws_bytes = k2w8::splitk_workspace_bytes();
+  hipError_t e = hipMalloc(&g->workspace, ws_bytes);
+  if (e != hipSuccess) return k2w8_fail_runtime("blocks_record: the graph's split-K workspace", e);
+  e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+  if (e != hipSuccess) return k2w8_fail_runtime(stage, e);
+  k2w8::splitk_install(k2w8::Workspace{g->workspace, ws_bytes});
+  for (int64_t i = 0; i < layers && rc == K2W8_OK; ++i) rc = run_block(stream, cfg, i, weights + i, buffers);
+  k2w8::splitk_install(k2w8::Workspace{});
   e = hipStreamEndCapture(s, &g->graph);
   if (rc != K2W8_OK) return rc;
   if (e != hipSuccess) return k2w8_fail_runtime(stage, e);

@@ -596,14 +596,14 @@ namespace {
 // Split K over 128x128 tiles when they would leave most CUs idle: enough slices to
 // give every CU a workgroup, each at least K2W8_SPLITK_MIN_STEPS K steps, within the
 // workspace. Returns the K steps per slice, or 0 for no split.
-int splitk_steps(const GemmLaunch &l, int64_t cus) {
+int splitk_steps(const GemmLaunch &l, int64_t cus, size_t workspace_bytes) {
   const int64_t tiles = ((l.m + 127) / 128) * (l.n / 128);
   const int64_t k_steps = l.k / 128;
   if (tiles * 2 > cus || k_steps < 2 * K2W8_SPLITK_MIN_STEPS) return 0;
   int64_t splits = (cus + tiles - 1) / tiles;
   if (splits > k_steps / K2W8_SPLITK_MIN_STEPS) splits = k_steps / K2W8_SPLITK_MIN_STEPS;
   const int64_t slice_bytes = l.m * l.n * 4;
-  const int64_t fit = (int64_t)splitk_workspace_bytes() / slice_bytes;
+  const int64_t fit = (int64_t)workspace_bytes / slice_bytes;
   if (splits > fit) splits = fit;
   if (splits < 2) return 0;
   const int64_t per = (k_steps + splits - 1) / splits;
@@ -672,10 +672,11 @@ hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &l) {
   // split-K pass over 128x128 tiles moves fewer bytes.
   if (tiles(64, 64) >= kCus && l.k <= 4096)
     return gemm::launch_tile<64, 64, 2, 2, 128, kS64Stages>(epilogue, stream, a);
-  const int per = splitk_steps(l, kCus);
+  const Workspace ws = l.workspace ? *l.workspace : splitk_workspace(stream);
+  const int per = ws.ptr ? splitk_steps(l, kCus, ws.bytes) : 0;
   if (per > 0) {
-    int32_t *parts = static_cast<int32_t *>(splitk_workspace(stream));
-    if (parts) {
+    int32_t *parts = static_cast<int32_t *>(ws.ptr);
+    {
       const int splits = (int)((l.k / 128 + per - 1) / per);
       gemm::GemmArgs p = a;
       p.c = parts;

@@ -23,6 +23,12 @@ hipError_t configure_prepare_lds();
 // inside a stream capture.
 hipError_t prepare_gated_ready(hipStream_t stream);
 
+// Device memory for the split-K GEMMs' int32 partial sums.
+struct Workspace {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+};
+
 enum Epilogue { kEpiPlain = 0, kEpiResid = 1, kEpiSwiglu = 2, kEpiBias = 3, kEpiAcc = 4 };
 
 struct GemmLaunch {
@@ -33,6 +39,8 @@ struct GemmLaunch {
   const void *bias = nullptr;    // bias
   int64_t m = 0, n = 0, k = 0, lda = 0;
   int m_group = 4;
+  // Split-K workspace for this call; unset (nullptr): splitk_workspace(stream).
+  const Workspace *workspace = nullptr;
 };
 
 hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &g);
@@ -70,10 +78,18 @@ hipError_t launch_attention(hipStream_t stream, const AttentionLaunch &l);
 // Multiprocessor (CU) count of the current device, cached per device ordinal.
 int device_cus();
 
-// The split-K GEMMs' int32 partial-sum workspace of the current device: allocated on
-// first use (never while `stream` is capturing; nullptr then, and the GEMM runs
-// without split-K), kept until the process ends.
+// Bytes of the workspace the library allocates for a stream (and for a recorded graph).
 size_t splitk_workspace_bytes();
-void *splitk_workspace(hipStream_t stream);
+// The workspace of a call on `stream` (current device), in order: the one a recording
+// on this thread has installed, the caller's registered for (device, stream), the
+// library's own for (device, stream), allocated on first use. Never allocates while
+// `stream` is capturing: {nullptr, 0} then, and the GEMM runs without split-K.
+Workspace splitk_workspace(hipStream_t stream);
+// Register caller-owned memory as the workspace of (current device, stream); a null
+// ptr removes the registration.
+hipError_t splitk_register(hipStream_t stream, void *ptr, size_t bytes);
+// The workspace every split-K call on this thread uses while a recording is being
+// captured (nullptr ptr: none installed).
+void splitk_install(Workspace ws);
 
 }  // namespace k2w8

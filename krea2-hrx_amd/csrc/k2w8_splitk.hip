@@ -6,10 +6,12 @@
 // (kernels/gemm_i8_256.loom:606-626, kernels/gemm_i8_resid_256.loom:623-635,
 // kernels/gemm_i8_swiglu_256.loom:640-660).
 //
-// The workspace is one device allocation per (device, stream), made on first use
-// outside any stream capture and kept for the life of the process. Calls on one
-// stream are ordered, so they may share it; calls on different streams get their own
-// and never race on it.
+// The workspace of a call is, in order: the buffer a graph recording installs for its
+// capture (each recorded graph owns one, so replays never share partial sums with
+// eager calls), a buffer the caller registered for (device, stream), or one device
+// allocation per (device, stream) made on first use outside any stream capture and
+// kept for the life of the process. Calls on one stream are ordered, so they may share
+// a stream's workspace; calls on different streams get their own and never race on it.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -131,30 +133,51 @@ __global__ __launch_bounds__(256) void reduce_kernel(ReduceArgs r) {
 
 constexpr size_t kWorkspaceBytes = size_t(64) << 20;
 std::mutex g_lock;
-std::map<std::pair<int, uintptr_t>, void *> g_workspace;  // (device, stream) -> buffer
+// (device, stream) -> the library's own buffer, and -> the caller's registered one
+std::map<std::pair<int, uintptr_t>, void *> g_owned;
+std::map<std::pair<int, uintptr_t>, Workspace> g_registered;
+thread_local Workspace t_installed;
 
 }  // namespace splitk
 
 size_t splitk_workspace_bytes() { return splitk::kWorkspaceBytes; }
 
-void *splitk_workspace(hipStream_t stream) {
+void splitk_install(Workspace ws) { splitk::t_installed = ws; }
+
+hipError_t splitk_register(hipStream_t stream, void *ptr, size_t bytes) {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
   const auto key = std::make_pair(dev, reinterpret_cast<uintptr_t>(stream));
   std::lock_guard<std::mutex> guard(splitk::g_lock);
-  const auto it = splitk::g_workspace.find(key);
-  if (it != splitk::g_workspace.end()) return it->second;
+  if (ptr)
+    splitk::g_registered[key] = Workspace{ptr, bytes};
+  else
+    splitk::g_registered.erase(key);
+  return hipSuccess;
+}
+
+Workspace splitk_workspace(hipStream_t stream) {
+  if (splitk::t_installed.ptr) return splitk::t_installed;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return Workspace{};
+  const auto key = std::make_pair(dev, reinterpret_cast<uintptr_t>(stream));
+  std::lock_guard<std::mutex> guard(splitk::g_lock);
+  const auto reg = splitk::g_registered.find(key);
+  if (reg != splitk::g_registered.end()) return reg->second;
+  const auto it = splitk::g_owned.find(key);
+  if (it != splitk::g_owned.end()) return Workspace{it->second, splitk::kWorkspaceBytes};
   // Never allocate inside a stream capture: the caller then runs without split-K.
   hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
-  if (stream && hipStreamIsCapturing(stream, &status) != hipSuccess) return nullptr;
-  if (status != hipStreamCaptureStatusNone) return nullptr;
+  if (stream && hipStreamIsCapturing(stream, &status) != hipSuccess) return Workspace{};
+  if (status != hipStreamCaptureStatusNone) return Workspace{};
   void *p = nullptr;
   if (hipMalloc(&p, splitk::kWorkspaceBytes) != hipSuccess) {
     (void)hipGetLastError();
-    return nullptr;
+    return Workspace{};
   }
-  splitk::g_workspace[key] = p;
-  return p;
+  splitk::g_owned[key] = p;
+  return Workspace{p, splitk::kWorkspaceBytes};
 }
 
 hipError_t launch_splitk_reduce(int epilogue, hipStream_t stream, const int32_t *parts, int splits,

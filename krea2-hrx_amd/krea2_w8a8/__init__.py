@@ -24,6 +24,8 @@ from .ops import (  # noqa: F401
     gemm_i8_resid,
     gemm_i8_resid_256x256,
     gemm_i8_swiglu,
+    gemm_set_workspace,
+    gemm_workspace_bytes,
     lora_transport,
     sigmoid_f32,
     prepare_gated_i8,
@@ -47,6 +49,8 @@ __all__ = [
     "gemm_i8_resid",
     "gemm_i8_resid_256x256",
     "gemm_i8_swiglu",
+    "gemm_set_workspace",
+    "gemm_workspace_bytes",
     "lib",
     "library_path",
     "lora_transport",

@@ -189,6 +189,26 @@ def gemm_i8_acc(a, w, acc, *, cfg: GemmConfig, m=None, stream=None):
     check(lib().k2w8_gemm_i8_acc(_stream(stream), ctypes.byref(k), m, pa, pw, out))
 
 
+def gemm_set_workspace(workspace, *, stream=None):
+    """Hand the GEMMs on ``stream`` (default: torch's current stream) a caller-owned
+    split-K workspace (a device tensor; its bytes are used, its dtype is not), or remove
+    the registration with ``None``. The caller keeps the tensor alive while it is
+    registered and while enqueued work may use it."""
+    if workspace is None:
+        check(lib().k2w8_gemm_set_workspace(_stream(stream), None, 0))
+        return
+    if not workspace.is_cuda or not workspace.is_contiguous():
+        raise InvalidArgument("workspace must be a contiguous device tensor")
+    nbytes = workspace.numel() * workspace.element_size()
+    check(lib().k2w8_gemm_set_workspace(_stream(stream), ctypes.c_void_p(workspace.data_ptr()),
+                                        nbytes))
+
+
+def gemm_workspace_bytes() -> int:
+    """Size of the split-K workspace the library allocates per stream."""
+    return int(lib().k2w8_gemm_workspace_bytes())
+
+
 def lora_transport(x, out, *, reverse: int, count=None, stream=None):
     """The 16-bit format change of kernels/native/lora_transport.loom: ``reverse`` 1 turns
     bf16 ``x`` into f16 ``out``, 2 turns f16 into bf16 (round to nearest even)."""

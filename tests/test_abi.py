@@ -35,7 +35,7 @@ def test_every_declared_entry_point_is_exported_and_bound(k2):
     for name in names:
         assert hasattr(lib, name), name
         assert name in k2._lib.SIGNATURES, name
-    assert lib.k2w8_abi_version() == 2
+    assert lib.k2w8_abi_version() == 3
 
 
 def test_shape_rules_are_the_reference_rules(k2):
