@@ -188,6 +188,20 @@ int k2w8_gemm_set_workspace(void *stream, void *workspace, int64_t bytes);
 int64_t k2w8_gemm_workspace_bytes(void);
 
 /*
+ * gemm_i8_noalloc: no counterpart in the reference. For callers that cannot allocate
+ * (code under graph capture, tight serving loops, harnesses that forbid hipMalloc):
+ * k2w8_gemm_i8 with the same arguments and bit-identical results, whose split-K
+ * partial sums go to a 16 MiB static device array of the library (one per device,
+ * held until the process ends) instead of any workspace, so no call allocates
+ * device memory. A shape that would split K into slices of which two do not fit
+ * (2 * m * n_size * 4 bytes > 16 MiB) is refused with INVALID_ARGUMENT; the split
+ * rule of this build never picks one. Every call on a device shares that device's
+ * array: calls that overlap on one device (on different streams) race on it.
+ */
+int k2w8_gemm_i8_noalloc(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, const int8_t *a,
+                         const int8_t *w, const float *scale, const float *a_scale, void *c);
+
+/*
  * lora_transport: replaces krea2_lora_transport (kernels/native/lora_transport.loom:5-41),
  * the 16-bit format change around the W8A8 projection of src/training/quantized.rs:66-105.
  * Each element is widened exactly to f32 and rounded (nearest even) to the other format.

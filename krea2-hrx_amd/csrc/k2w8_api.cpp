@@ -106,7 +106,7 @@ int check_gemm(const char *stage, const k2w8_gemm_cfg *cfg, int64_t m, const int
 
 int run_gemm(const char *stage, int epi, void *stream, const k2w8_gemm_cfg *cfg, int64_t m,
              const int8_t *a, const int8_t *w, const float *scale, const float *a_scale, void *c,
-             const float *gate, const void *bias) {
+             const float *gate, const void *bias, const k2w8::Workspace *fixed = nullptr) {
   int rc = check_gemm(stage, cfg, m, a, w, scale, a_scale, c);
   if (rc != K2W8_OK) return rc;
   if (epi == k2w8::kEpiResid && !gate) return fail(K2W8_INVALID_ARGUMENT, "%s: null gate", stage);
@@ -127,7 +127,15 @@ int run_gemm(const char *stage, int epi, void *stream, const k2w8_gemm_cfg *cfg,
   l.k = cfg->k_size;
   l.lda = cfg->k_stride;
   l.m_group = (int)cfg->m_group;
+  l.workspace = fixed;
+  l.workspace_required = fixed != nullptr;
   hipError_t e = k2w8::launch_gemm(epi, static_cast<hipStream_t>(stream), l);
+  if (e == hipErrorInvalidValue && fixed)
+    return fail(K2W8_INVALID_ARGUMENT,
+                "%s: m=%lld x n_size=%lld splits K and needs %lld bytes of scratch for two int32 "
+                "slices; the static scratch holds %lld", stage, (long long)m,
+                (long long)cfg->n_size, (long long)(2 * m * cfg->n_size * 4),
+                (long long)fixed->bytes);
   if (e != hipSuccess) return runtime(stage, e);
   return ok();
 }
@@ -263,6 +271,18 @@ int k2w8_gemm_i8_bias(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, const i
                       void *c) {
   return run_gemm("gemm_i8_bias", k2w8::kEpiBias, stream, cfg, m, a, w, scale, a_scale, c,
                   nullptr, bias);
+}
+
+int k2w8_gemm_i8_noalloc(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, const int8_t *a,
+                         const int8_t *w, const float *scale, const float *a_scale, void *c) {
+  const char *stage = "gemm_i8_noalloc";
+  int rc = check_gemm(stage, cfg, m, a, w, scale, a_scale, c);
+  if (rc != K2W8_OK) return rc;
+  hipError_t e = hipSuccess;
+  const k2w8::Workspace scratch = k2w8::splitk_static_scratch(&e);
+  if (e != hipSuccess) return runtime("gemm_i8_noalloc: the static scratch's device address", e);
+  return run_gemm(stage, k2w8::kEpiPlain, stream, cfg, m, a, w, scale, a_scale, c, nullptr,
+                  nullptr, &scratch);
 }
 
 int k2w8_gemm_set_workspace(void *stream, void *workspace, int64_t bytes) {

@@ -673,6 +673,11 @@ hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &l) {
   if (tiles(64, 64) >= kCus && l.k <= 4096)
     return gemm::launch_tile<64, 64, 2, 2, 128, kS64Stages>(epilogue, stream, a);
   const Workspace ws = l.workspace ? *l.workspace : splitk_workspace(stream);
+  // A caller that passes a fixed workspace and requires it: a shape that would split K
+  // but whose two slices do not fit is refused before anything is launched.
+  if (l.workspace_required && splitk_steps(l, kCus, SIZE_MAX) > 0 &&
+      (size_t)(2 * l.m * l.n * 4) > ws.bytes)
+    return hipErrorInvalidValue;
   const int per = ws.ptr ? splitk_steps(l, kCus, ws.bytes) : 0;
   if (per > 0) {
     int32_t *parts = static_cast<int32_t *>(ws.ptr);

@@ -41,6 +41,10 @@ struct GemmLaunch {
   int m_group = 4;
   // Split-K workspace for this call; unset (nullptr): splitk_workspace(stream).
   const Workspace *workspace = nullptr;
+  // With `workspace`: a shape that would split K into slices that do not fit (fewer
+  // than two) fails with hipErrorInvalidValue before any launch, instead of running
+  // unsplit.
+  bool workspace_required = false;
 };
 
 hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &g);
@@ -91,5 +95,9 @@ hipError_t splitk_register(hipStream_t stream, void *ptr, size_t bytes);
 // The workspace every split-K call on this thread uses while a recording is being
 // captured (nullptr ptr: none installed).
 void splitk_install(Workspace ws);
+// The allocation-free GEMM entry point's scratch: a static device array, one per
+// device. Its address on the current device is looked up once per device; `err`
+// receives the lookup's failure.
+Workspace splitk_static_scratch(hipError_t *err);
 
 }  // namespace k2w8

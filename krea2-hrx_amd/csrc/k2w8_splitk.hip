@@ -140,6 +140,34 @@ thread_local Workspace t_installed;
 
 }  // namespace splitk
 
+// Scratch of k2w8_gemm_i8_noalloc: a file-scope device array, so that entry point never
+// allocates. 16 MiB holds at least two K slices of every shape the split-K rule picks
+// (it splits only when 128x128 tiles cover at most half of the 256 CUs: m x n <= 2^21
+// outputs, 8 MiB of int32 per slice). Every call on a device shares that device's copy;
+// calls that overlap on one device race on it. Each slice overwrites its whole part, so
+// nothing needs clearing between calls.
+constexpr size_t kScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) int32_t scratch[kScratchBytes / sizeof(int32_t)];
+
+namespace splitk {
+std::map<int, void *> g_scratch;  // device -> the address of that device's `scratch`
+}  // namespace splitk
+
+Workspace splitk_static_scratch(hipError_t *err) {
+  *err = hipSuccess;
+  int dev = 0;
+  if ((*err = hipGetDevice(&dev)) != hipSuccess) return Workspace{};
+  std::lock_guard<std::mutex> guard(splitk::g_lock);
+  const auto it = splitk::g_scratch.find(dev);
+  if (it != splitk::g_scratch.end()) return Workspace{it->second, kScratchBytes};
+  // The array's name is a host-side stand-in; the device copy's address comes from the
+  // runtime, once per device, with that device current.
+  void *p = nullptr;
+  if ((*err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess) return Workspace{};
+  splitk::g_scratch[dev] = p;
+  return Workspace{p, kScratchBytes};
+}
+
 size_t splitk_workspace_bytes() { return splitk::kWorkspaceBytes; }
 
 void splitk_install(Workspace ws) { splitk::t_installed = ws; }

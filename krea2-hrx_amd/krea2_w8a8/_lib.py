@@ -147,6 +147,7 @@ SIGNATURES = {
     "k2w8_gemm_i8_bias": (ctypes.c_int, [_P, ctypes.POINTER(GemmCfg), _I64, _P, _P, _P, _P, _P, _P]),
     "k2w8_gemm_i8_acc": (ctypes.c_int, [_P, ctypes.POINTER(GemmCfg), _I64, _P, _P, _P]),
     "k2w8_gemm_set_workspace": (ctypes.c_int, [_P, _P, _I64]),
+    "k2w8_gemm_i8_noalloc": (ctypes.c_int, [_P, ctypes.POINTER(GemmCfg), _I64, _P, _P, _P, _P, _P]),
     "k2w8_gemm_workspace_bytes": (_I64, []),
     "k2w8_lora_transport": (ctypes.c_int, [_P, ctypes.c_int, _I64, _P, _P]),
     "k2w8_sigmoid_f32": (ctypes.c_int, [_P, _I64, _P, _P]),
