@@ -213,7 +213,7 @@ def main():
             "bound": "mfma",
             "achieved": round(gemm_tops, 1),
             "peak": PEAK_INT8_TOPS,
-            "unit": "TFLOP/s",
+            "unit": "TOPS",
             "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
             "traffic": measured_traffic(),
             "algorithmic_bytes": gemm_bytes,
@@ -237,6 +237,8 @@ def main():
         result["attention_production"] = attention_production(k2, torch, args)
         torch.cuda.empty_cache()
         result["config5_skinny"] = skinny_sweep(k2, torch, weights, hidden, args)
+        torch.cuda.empty_cache()
+        result["production_gemms"] = production_gemms(k2, torch, args)
         torch.cuda.empty_cache()
 
     if not args.no_cpu:
@@ -294,35 +296,46 @@ def batch_timed(torch, fn, steps, warmup):
     return e0.elapsed_time(e1) * 1e-3 / steps
 
 
-def timed(torch, fn, steps, warmup):
-    for i in range(warmup):
-        fn(i)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(steps):
-        fn(i)
-    torch.cuda.synchronize()
-    return (time.perf_counter() - t0) / steps
-
-
 def north_star(k2, torch, weights, hidden, args):
-    """The target GEMM alone: M=4096, K=3072, N=12288, plain epilogue."""
+    """The target GEMM: M=4096, K=3072, N=12288, plain epilogue, timed by HIP events on the
+    launch stream. Its A operand is what the path feeds it: f16 N(0,1) rows with 8
+    outlier channels x20 through prepare_plain_i8 (the north star's prepare -> GEMM).
+    The MFMAs' power, and so the clock the chip holds, depends on the operand bytes, so
+    the same GEMM on uniform random int8 A (every bit toggling) is reported beside it."""
     M, K, N = 4096, 3072, 12288
     copies = 3
-    a = [torch.randint(-127, 128, (M, K), device="cuda", dtype=torch.int8) for _ in range(copies)]
-    s = [torch.rand(M, device="cuda") * 1e-2 + 1e-3 for _ in range(copies)]
+    hs = [hidden(M, K, 3100 + c).to(torch.float16) for c in range(copies)]
+    a = [torch.empty((M, K), device="cuda", dtype=torch.int8) for _ in range(copies)]
+    s = [torch.empty(M, device="cuda") for _ in range(copies)]
+    for c in range(copies):
+        k2.prepare_plain_i8(hs[c], a[c], s[c], width=K, out_stride=K)
+    au = [torch.randint(-127, 128, (M, K), device="cuda", dtype=torch.int8) for _ in range(copies)]
     ws = [weights(N, K, 3000 + c) for c in range(copies)]
     out = [torch.empty((M, N), dtype=torch.float16, device="cuda") for _ in range(copies)]
     cfg = k2.GemmConfig(k_size=K, n_size=N, k_stride=K)
 
-    def fn(i):
+    def gemm(i, ops=a):
         c = i % copies
-        k2.gemm_i8(a[c], ws[c][0], ws[c][1], s[c], out[c], cfg=cfg)
+        k2.gemm_i8(ops[c], ws[c][0], ws[c][1], s[c], out[c], cfg=cfg)
 
-    sec = timed(torch, fn, args.steps, args.warmup)
-    tops = 2.0 * M * N * K / sec / 1e12
+    def chain(i):
+        c = i % copies
+        k2.prepare_plain_i8(hs[c], a[c], s[c], width=K, out_stride=K)
+        gemm(i)
+
+    sec = event_timed(torch, gemm, args.steps, args.warmup)
+    sec_u = event_timed(torch, lambda i: gemm(i, au), args.steps, args.warmup)
+    sec_c = event_timed(torch, chain, args.steps, args.warmup)
+    ops = 2.0 * M * N * K
+    tops = ops / sec / 1e12
     return {"M": M, "K": K, "N": N, "us": round(sec * 1e6, 2), "TOPS": round(tops, 1),
-            "pct_of_int8_peak": round(100 * tops / PEAK_INT8_TOPS, 2), "target_pct": 60.0}
+            "pct_of_int8_peak": round(100 * tops / PEAK_INT8_TOPS, 2), "target_pct": 60.0,
+            "a_operand": "prepare_plain_i8 of f16 N(0,1) rows with 8 outlier channels x20",
+            "us_uniform_a": round(sec_u * 1e6, 2),
+            "pct_of_int8_peak_uniform_a": round(100 * ops / sec_u / 1e12 / PEAK_INT8_TOPS, 2),
+            "us_prepare_plus_gemm": round(sec_c * 1e6, 2),
+            "pct_of_int8_peak_prepare_plus_gemm": round(100 * ops / sec_c / 1e12 / PEAK_INT8_TOPS, 2),
+            "timing": "HIP events on the launch stream around each call, mean"}
 
 
 def single_gemm(k2, torch, weights, hidden, args):
@@ -343,9 +356,9 @@ def single_gemm(k2, torch, weights, hidden, args):
         k2.prepare_plain_i8(h, q, qs, width=K, out_stride=K)
         k2.gemm_i8_bias(q, w, ws, qs, bias, out, cfg=cfg)
 
-    sec = timed(torch, fn, args.steps, args.warmup)
-    gsec = timed(torch, lambda _: k2.gemm_i8_bias(q, w, ws, qs, bias, out, cfg=cfg), args.steps,
-                 args.warmup)
+    sec = event_timed(torch, fn, args.steps, args.warmup)
+    gsec = event_timed(torch, lambda _: k2.gemm_i8_bias(q, w, ws, qs, bias, out, cfg=cfg),
+                       args.steps, args.warmup)
     ops = 2.0 * M * N * K
     return {"M": M, "K": K, "N": N, "us_prepare_plus_gemm": round(sec * 1e6, 2),
             "us_gemm": round(gsec * 1e6, 2), "TOPS_gemm": round(ops / gsec / 1e12, 1),
@@ -374,10 +387,58 @@ def mlp_pair(k2, torch, weights, hidden, args):
         k2.prepare_plain_i8(up, q, qs, width=I, out_stride=pitch_i)
         k2.gemm_i8_resid_256x256(q, wd, sd, qs, x, one, cfg=c_d)
 
-    sec = timed(torch, fn, max(2, args.steps // 2), max(1, args.warmup // 2))
+    sec = event_timed(torch, fn, max(2, args.steps // 2), max(1, args.warmup // 2))
     ops = 2.0 * M * H * 2 * I + 2.0 * M * I * H
     return {"M": M, "ms": round(sec * 1e3, 4), "TOPS": round(ops / sec / 1e12, 1),
             "pct_of_int8_peak": round(100 * ops / sec / 1e12 / PEAK_INT8_TOPS, 2)}
+
+
+def production_gemms(k2, torch, args):
+    """The reference's own GEMM benchmark matrix (benches/kernels.rs:58-64): the four
+    production projections at hidden 6144 -- qkvg (K=6144, N=15360), gate|up + SwiGLU
+    (N=32768), wo + residual (6144x6144) and down + residual (K=16384, pitch 16448, its
+    256x256 kernel) -- at M in {1043, 4095, 4096, 4109, 12301, 16397}, with that bench's
+    operands (bytes (73 i + salt) mod 255 within K, zero padding; scales 1e-3 / 1e-2,
+    residual gate 0.25). Times are HIP events on the launch stream, mean per call."""
+    rows = []
+    for name, k, n, kind in [("gemm_qkvg", 6144, 15360, "plain"), ("gemm_gu", 6144, 32768, "swiglu"),
+                             ("gemm_wo", 6144, 6144, "resid"), ("gemm_down", 16384, 6144, "resid_wide")]:
+        pitch = int(k2.shape.gemm_pitch(k))
+
+        def operand(r, salt):
+            i = torch.arange(r * pitch, device="cuda", dtype=torch.int64)
+            v = ((i * 73 + salt) % 255).to(torch.uint8).view(torch.int8).reshape(r, pitch)
+            v[:, k:] = 0
+            return v
+
+        w = operand(n, 31)
+        ws = torch.full((n,), 1e-3, device="cuda")
+        gate = torch.full((n,), 0.25, device="cuda")
+        for m in (1043, 4095, 4096, 4109, 12301, 16397):
+            a = operand(m, 17)
+            sc = torch.full((m,), 1e-2, device="cuda")
+            cfg = k2.GemmConfig(k_size=k, n_size=n, k_stride=pitch,
+                                schedule_rows=int(k2.shape.gemm_schedule_rows(m)))
+            if kind == "swiglu":
+                out = torch.empty((m, n // 2), dtype=torch.float16, device="cuda")
+                fn = lambda _: k2.gemm_i8_swiglu(a, w, ws, sc, out, cfg=cfg)  # noqa: E731
+            elif kind == "plain":
+                out = torch.empty((m, n), dtype=torch.float16, device="cuda")
+                fn = lambda _: k2.gemm_i8(a, w, ws, sc, out, cfg=cfg)  # noqa: E731
+            else:
+                out = torch.zeros((m, n), dtype=torch.bfloat16, device="cuda")
+                op = k2.gemm_i8_resid if kind == "resid" else k2.gemm_i8_resid_256x256
+                fn = lambda _: op(a, w, ws, sc, out, gate, cfg=cfg)  # noqa: E731
+            steps = max(3, min(args.steps, 20))
+            sec = event_timed(torch, fn, steps, 2)
+            tops = 2.0 * m * n * k / sec / 1e12
+            rows.append({"gemm": name, "M": m, "K": k, "N": n, "us": round(sec * 1e6, 2),
+                         "TOPS": round(tops, 1),
+                         "pct_of_int8_peak": round(100 * tops / PEAK_INT8_TOPS, 2)})
+            del a, out
+        del w
+        torch.cuda.empty_cache()
+    return rows
 
 
 COLD_BYTES = 320 << 20  # weight copies rotated per call: more than the 256 MB MALL
@@ -559,13 +620,13 @@ def cpu_baseline(M, K, N, pitch, budget_s):
     ns = (rng.uniform(0.5, 1.5, K) - 1.0).astype(np.float32)
     z = np.zeros(K, np.float32)
 
-    def run(rows):
+    def run(rows, nt=threads):
         x = rng.standard_normal((rows, K)).astype(np.float32)
         u = x.astype(np.float16).astype(np.float32).view(np.uint32).astype(np.uint64)
         h = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
         t0 = time.perf_counter()
-        q, s = oracle.prepare_norm(h, ns, z, z, K, pitch, 1e-6, threads=threads)
-        oracle.gemm_i8(q, w, rows, N, K, pitch, ws, s, threads=threads)
+        q, s = oracle.prepare_norm(h, ns, z, z, K, pitch, 1e-6, threads=nt)
+        oracle.gemm_i8(q, w, rows, N, K, pitch, ws, s, threads=nt)
         return time.perf_counter() - t0
 
     rows = 64
@@ -577,9 +638,29 @@ def cpu_baseline(M, K, N, pitch, budget_s):
     times = sorted(run(rows) for _ in range(reps))
     t = times[len(times) // 2]
     tops = 2.0 * rows * N * K / t / 1e12
+    # One thread: the same step on a sample of about a quarter of the budget.
+    rows1 = 16
+    t1 = run(rows1, 1)
+    rows1 = int(max(16, min(M, rows1 * budget_s / 4 / max(t1, 1e-3))))
+    t1 = run(rows1, 1)
     return {"value": round(tops, 5), "unit": "TOPS", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"{rows} of {M} tokens through prepare_norm_i8 + gemm_i8 (K={K}, N={N}), "
-                      f"median of {reps} repetitions of {t:.2f} s"}
+                      f"median of {reps} repetitions of {t:.2f} s",
+            "single_thread": {"value": round(2.0 * rows1 * N * K / t1 / 1e12, 6), "unit": "TOPS",
+                              "cores": 1,
+                              "sample": f"{rows1} of {M} tokens, one run of {t1:.2f} s"}}
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 if __name__ == "__main__":

@@ -126,6 +126,20 @@ float ora_expf(float x) {
 void ora_expf_n(const float *x, float *y, int64_t n) {
     for (int64_t i = 0; i < n; ++i) y[i] = ora_expf(x[i]);
 }
+/* sigmoid(g) = 1 / (1 + exp(-g)) with this file's exp and IEEE f32 division: the
+ * function of kernels/prepare_gated_i8.loom:97-101 and kernels/gemm_i8_swiglu_256.loom:
+ * 649-652 with expf<afn> replaced by ora_expf. Bit patterns of all 2^32 inputs from
+ * `first` on are generated here (y[i] = sigmoid(bits first + i)), multithreaded. */
+void ora_sigmoid_bits_n(uint32_t first, float *y, int64_t n) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        const uint32_t b = first + (uint32_t)i;
+        float g;
+        memcpy(&g, &b, 4);
+        y[i] = 1.0f / (1.0f + ora_expf(0.0f - g));
+    }
+}
+
 void ora_f16_from_f32_n(const float *x, uint16_t *y, int64_t n) {
     for (int64_t i = 0; i < n; ++i) y[i] = ora_f16_from_f32(x[i]);
 }

@@ -31,6 +31,7 @@ float ora_expf(float x);
 
 /* Element-wise helpers exposed so tests can check them in bulk. */
 void ora_expf_n(const float *x, float *y, int64_t n);
+void ora_sigmoid_bits_n(uint32_t first, float *y, int64_t n);
 void ora_f16_from_f32_n(const float *x, uint16_t *y, int64_t n);
 void ora_bf16_from_f32_n(const float *x, uint16_t *y, int64_t n);
 

@@ -35,6 +35,7 @@ def lib() -> ctypes.CDLL:
             "ora_f16_from_f32": (ctypes.c_uint16, [F]),
             "ora_expf": (F, [F]),
             "ora_expf_n": (None, [P, P, I]),
+            "ora_sigmoid_bits_n": (None, [ctypes.c_uint32, P, I]),
             "ora_f16_from_f32_n": (None, [P, P, I]),
             "ora_bf16_from_f32_n": (None, [P, P, I]),
             "ora_prepare_plain_i8": (None, [I, I, I, P, P, P, ctypes.c_int]),
@@ -70,6 +71,13 @@ def expf(x: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     y = np.empty_like(x)
     lib().ora_expf_n(_p(x), _p(y), x.size)
+    return y
+
+
+def sigmoid_of_bits(first: int, count: int) -> np.ndarray:
+    """sigmoid of the f32 values with bit patterns first, first + 1, ... (count of them)."""
+    y = np.empty(count, np.float32)
+    lib().ora_sigmoid_bits_n(first, _p(y), count)
     return y
 
 

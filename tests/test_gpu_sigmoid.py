@@ -65,3 +65,21 @@ def test_device_sigmoid_is_bit_identical_to_the_cpu_definition():
                             want[~nan][diff][:8])
     # the bands above do reach the division path and subnormal quotients
     assert (want[~nan] < np.float32(2.0 ** -126)).any() and (want == 0).any()
+
+
+def test_device_sigmoid_over_every_f32_input():
+    # All 2^32 bit patterns, in chunks of 2^28: the device function against the oracle's
+    # definition (ora_sigmoid_bits_n), bit for bit; NaN inputs give NaN on both.
+    chunk = 1 << 28
+    out = torch.empty(chunk, dtype=torch.float32, device="cuda")
+    for c in range((1 << 32) // chunk):
+        first = c * chunk
+        start = first if first < (1 << 31) else first - (1 << 32)
+        x = torch.arange(start, start + chunk, dtype=torch.int32, device="cuda").view(torch.float32)
+        k2.sigmoid_f32(x, out)
+        got = out.cpu().numpy()
+        want = oracle.sigmoid_of_bits(first, chunk)
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got), nan), c
+        diff = got.view(np.uint32)[~nan] != want.view(np.uint32)[~nan]
+        assert not diff.any(), (c, int(diff.sum()))
