@@ -222,3 +222,53 @@ def test_config4_skinny_sweep(m, gemm):
     sync()
     assert np.array_equal(host(q), q_ref)
     assert np.array_equal(host(out).reshape(want.shape), want)
+
+
+PRODUCTION = [(name, m) for name in ("gemm_qkvg", "gemm_gu", "gemm_wo", "gemm_down")
+              for m in (12301, 16397)]
+
+
+@pytest.mark.parametrize("name,m", PRODUCTION)
+def test_production_gemm_at_the_largest_token_counts(name, m):
+    # The reference's bench matrix (benches/kernels.rs:58-64) at M=12301 and 16397 (ragged
+    # 256-row tiles; the most tile rounds). Full-size int64 row and column checksums of
+    # the int32 accumulators (size-independent identities), then 40 rows (two per 1024,
+    # the first and the last) exact through the production epilogue against the oracle.
+    k, n, kind = {"gemm_qkvg": (6144, 15360, "plain"), "gemm_gu": (6144, 32768, "swiglu"),
+                  "gemm_wo": (6144, 6144, "resid"), "gemm_down": (16384, 6144, "resid_wide")}[name]
+    rng = np.random.default_rng(7000 + m + k + n)
+    pitch = int(k2.shape.gemm_pitch(k))
+    a = int8_weights(rng, m, k, pitch)
+    w = int8_weights(rng, n, k, pitch)
+    ws = channel_scales(rng, n)
+    sc = rng.uniform(1e-3, 3e-2, m).astype(np.float32)
+    A, W = dev(a), dev(w)
+    c = cfg(k, n, pitch, int(k2.shape.gemm_schedule_rows(m)))
+    acc = torch.empty((m, n), dtype=torch.int32, device="cuda")
+    k2.gemm_i8_acc(A, W, acc, cfg=c)
+    Ak, Wk = A[:, :k].to(torch.int64), W[:, :k].to(torch.int64)
+    assert torch.equal(acc.to(torch.int64).sum(1), (Ak * Wk.sum(0)).sum(1))
+    assert torch.equal(acc.to(torch.int64).sum(0), (Wk * Ak.sum(0)).sum(1))
+    del Ak, Wk
+    rows = np.unique(np.concatenate([rng.choice(m, 38, replace=False), [0, m - 1]]))
+    ref = oracle.gemm_i32(a[rows], w, len(rows), n, k, pitch)
+    pick = torch.from_numpy(rows).cuda()
+    assert np.array_equal(host(acc[pick]), ref)
+    del acc
+    if kind == "plain":
+        out = torch.empty((m, n), dtype=torch.float16, device="cuda")
+        k2.gemm_i8(A, W, dev(ws), dev(sc), out, cfg=c)
+        want = oracle.epilogue_plain(ref, ws, sc[rows])
+    elif kind == "swiglu":
+        out = torch.empty((m, n // 2), dtype=torch.float16, device="cuda")
+        k2.gemm_i8_swiglu(A, W, dev(ws), dev(sc), out, cfg=c)
+        want = oracle.epilogue_swiglu(ref, ws, sc[rows])
+    else:
+        x0 = bf16_bits(rng.standard_normal((m, n)).astype(np.float32))
+        gate = rng.uniform(0.5, 1.5, n).astype(np.float32)
+        out = dev(x0, torch.bfloat16)
+        op = k2.gemm_i8_resid if kind == "resid" else k2.gemm_i8_resid_256x256
+        op(A, W, dev(ws), dev(sc), out, dev(gate), cfg=c)
+        want = oracle.epilogue_resid(ref, ws, sc[rows], gate, x0[rows])
+    sync()
+    assert np.array_equal(host(out[pick]), want)
