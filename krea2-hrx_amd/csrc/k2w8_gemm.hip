@@ -289,7 +289,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
   constexpr int kStage = (BM + BN) * BK;
   constexpr int kIns = kAIns + kBIns;
   static_assert(kAIns * kWaves * 1024 == BM * BK && kBIns * kWaves * 1024 == BN * BK, "staging");
-  static_assert(BK % 32 == 0 && STAGES >= 2, "pipeline");
+  static_assert(BK % 32 == 0 && STAGES >= 2 && kWaves % 2 == 0, "pipeline");
   extern __shared__ __align__(16) uint8_t smem[];
 
   const int tid = threadIdx.x;
@@ -300,12 +300,22 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
   tile_of(blockIdx.x, (g.m + BM - 1) / BM, g.n / BN, g.m_group, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
 
-  // Transfers: wave w's instruction i fills 1 KiB block b = w*kAIns + i of the stage's
-  // A rows (then likewise B): rows b*kRowsPerKb + lane/kCpr, physical chunk lane%kCpr,
-  // which holds logical K chunk (lane%kCpr) ^ key(row). Ghost rows past m read row
-  // m-1; their results are never stored.
+  // Transfers. The stage's A rows are 1 KiB blocks, block b = v*kAIns + i for "virtual
+  // wave" v < kWaves (then likewise B): rows b*kRowsPerKb + lane/kCpr, physical chunk
+  // lane%kCpr, which holds logical K chunk (lane%kCpr) ^ key(row). Ghost rows past m read
+  // row m-1; their results are never stored. The lower half of the waves (one per SIMD)
+  // issue every transfer, for virtual waves w and w + kWaves/2: a transfer instruction
+  // holds up the issuing wave's next instructions for tens of cycles, and with the
+  // transfers on one wave of each SIMD the other wave keeps the MFMA pipe fed meanwhile
+  // (north star 159 -> 147 us against every wave issuing its own eighth).
+  // Four-wave tiles (one workgroup per CU pair of SIMDs or less, the mid-M shapes) keep
+  // every wave issuing its own share: there the transfers would crowd two SIMDs.
+  constexpr bool kSplitRoles = kWaves == 8;
+  constexpr int kHalf = kSplitRoles ? kWaves / 2 : kWaves;
+  constexpr int kPer = kSplitRoles ? 2 : 1;  // virtual waves per producer
+  const bool producer = wave < kHalf;
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
-  uint32_t a_off[kAIns], b_off[kBIns];
+  uint32_t a_off[kPer * kAIns], b_off[kPer * kBIns];
   // This workgroup's K steps (all of K, or its split's share).
   int kt_count = g.k / BK, kt_first = 0;
   if (g.k_split_steps > 0) {
@@ -313,27 +323,39 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
     kt_count = min(g.k_split_steps, kt_count - kt_first);
   }
   const uint32_t k_first = (uint32_t)(kt_first * BK);
+  const int vw0 = producer ? wave : wave - kHalf;  // first virtual wave of this wave
 #pragma unroll
-  for (int i = 0; i < kAIns; ++i) {
-    const int r = (wave * kAIns + i) * kRowsPerKb + lane / kCpr;
-    const int c = (lane % kCpr) ^ swz_key<BK>(r);
-    a_off[i] = (uint32_t)min(m0 + r, g.m - 1) * (uint32_t)g.lda + c * 16 + k_first;
-  }
+  for (int j = 0; j < kPer; ++j)
 #pragma unroll
-  for (int i = 0; i < kBIns; ++i) {
-    const int r = (wave * kBIns + i) * kRowsPerKb + lane / kCpr;
-    const int c = (lane % kCpr) ^ swz_key<BK>(r);
-    b_off[i] = (uint32_t)(n0 + r) * (uint32_t)g.lda + c * 16 + k_first;
-  }
-  const uint32_t a_lds = lds0 + wave * kAIns * 1024;
-  const uint32_t b_lds = lds0 + BM * BK + wave * kBIns * 1024;
+    for (int i = 0; i < kAIns; ++i) {
+      const int r = ((vw0 + j * kHalf) * kAIns + i) * kRowsPerKb + lane / kCpr;
+      const int c = (lane % kCpr) ^ swz_key<BK>(r);
+      a_off[j * kAIns + i] = (uint32_t)min(m0 + r, g.m - 1) * (uint32_t)g.lda + c * 16 + k_first;
+    }
+#pragma unroll
+  for (int j = 0; j < kPer; ++j)
+#pragma unroll
+    for (int i = 0; i < kBIns; ++i) {
+      const int r = ((vw0 + j * kHalf) * kBIns + i) * kRowsPerKb + lane / kCpr;
+      const int c = (lane % kCpr) ^ swz_key<BK>(r);
+      b_off[j * kBIns + i] = (uint32_t)(n0 + r) * (uint32_t)g.lda + c * 16 + k_first;
+    }
+  const uint32_t a_lds = lds0 + vw0 * kAIns * 1024;
+  const uint32_t b_lds = lds0 + BM * BK + vw0 * kBIns * 1024;
 
   auto issue = [&](int kt) {
+    if (!producer) return;
     const uint32_t so = (uint32_t)((kt % STAGES) * kStage), ko = (uint32_t)(kt * BK);
 #pragma unroll
-    for (int i = 0; i < kAIns; ++i) dma16(a_lds + so + i * 1024, g.a, a_off[i] + ko);
+    for (int j = 0; j < kPer; ++j)
 #pragma unroll
-    for (int i = 0; i < kBIns; ++i) dma16(b_lds + so + i * 1024, g.w, b_off[i] + ko);
+      for (int i = 0; i < kAIns; ++i)
+        dma16(a_lds + so + (j * kHalf * kAIns + i) * 1024, g.a, a_off[j * kAIns + i] + ko);
+#pragma unroll
+    for (int j = 0; j < kPer; ++j)
+#pragma unroll
+      for (int i = 0; i < kBIns; ++i)
+        dma16(b_lds + so + (j * kHalf * kBIns + i) * 1024, g.w, b_off[j * kBIns + i] + ko);
   };
 #pragma unroll
   for (int s = 0; s < STAGES; ++s)
@@ -374,8 +396,9 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
   constexpr int NS = BK / 32;
   static_assert(NS % 2 == 0, "slice parity must repeat per step");
   v4i af[2][FM], bf[2][FN];
-  if (STAGES >= 2) wait_vmcnt<(STAGES - 1) * kIns>();
+  // A producer's transfers per stage: kPer kIns; the others have none outstanding.
   if (kt_count < STAGES) wait_vmcnt<0>();
+  else if (producer) wait_vmcnt<(STAGES - 1) * kPer * kIns>();
   __builtin_amdgcn_s_barrier();
   read_frags<FM, FN>(af[0], bf[0], smem, a_row_off, b_row_off, (kh ^ rsw) << 4);
 
@@ -395,7 +418,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
       }
       if (s + 1 == NS && kt + 1 < kt_count) {
         if (kt + STAGES - 1 < kt_count)
-          wait_vmcnt<(STAGES - 2) * kIns>();
+          wait_vmcnt<(STAGES - 2) * kPer * kIns>();
         else
           wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
