@@ -35,6 +35,7 @@
 #include <stdint.h>
 
 #include <mutex>
+#include <type_traits>
 
 #include "k2w8_numerics.hpp"
 #include "k2w8_internal.hpp"
@@ -246,19 +247,27 @@ __global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArg
     __syncthreads();
   }
   const uint16_t *sigmoid_lds = reinterpret_cast<const uint16_t *>(factor_lds);
+  // Whether every modulation scale and shift is zero (plain RMSNorm, as in a block
+  // without adaLN): then b = a * bf16(1 + 0) = a and c = b + 0 = b are identities (a is
+  // already bf16; only the sign of a zero can change, which no code or scale sees),
+  // and the formula runs without them.
+  int modulated = 0;
   if (kLdsFactors) {
     for (int c = threadIdx.x; c < (width >> 2); c += blockDim.x) {
       const float4 a = reinterpret_cast<const float4 *>(args.norm_scale)[c];
       const float4 b = reinterpret_cast<const float4 *>(args.mod_scale)[c];
+      const float4 sh = reinterpret_cast<const float4 *>(args.mod_shift)[c];
+      modulated |= (b.x != 0.0f) | (b.y != 0.0f) | (b.z != 0.0f) | (b.w != 0.0f) |
+                   (sh.x != 0.0f) | (sh.y != 0.0f) | (sh.z != 0.0f) | (sh.w != 0.0f);
       float m0 = b.x + 1.0f, m1 = b.y + 1.0f, m2 = b.z + 1.0f, m3 = b.w + 1.0f;
       bf16_round2(m0, m1);
       bf16_round2(m2, m3);
       const int slot = kFactorStride * (c >> 2) + (c & 3);
       factor_lds[slot] = make_float4(a.x + 1.0f, a.y + 1.0f, a.z + 1.0f, a.w + 1.0f);
       factor_lds[slot + 4] = make_float4(m0, m1, m2, m3);
-      factor_lds[slot + 8] = reinterpret_cast<const float4 *>(args.mod_shift)[c];
+      factor_lds[slot + 8] = sh;
     }
-    __syncthreads();
+    modulated = __syncthreads_or(modulated);
   }
   auto factors = [&](int r, float (&ns1)[16], float (&ms1)[16], float (&shf)[16]) {
 #pragma unroll
@@ -290,7 +299,8 @@ __global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArg
   constexpr bool kEarlyPrefetch = !(kKind == kNorm && !kSingle);
 
   // One token of the team: compute `cur` while the next token's row loads into `nxt`.
-  auto step = [&](Raw<kKind, T> &cur, Raw<kKind, T> &nxt) __attribute__((always_inline)) {
+  auto step = [&](Raw<kKind, T> &cur, Raw<kKind, T> &nxt, auto mod_tag) __attribute__((always_inline)) {
+    constexpr bool kMod = decltype(mod_tag)::value;
     const bool live = token < args.tokens;
     const int next = token + stride;
     if (kEarlyPrefetch) load(nxt, next);
@@ -407,12 +417,16 @@ __global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArg
           float n0 = lo_bf16(word) * rms_inv, n1 = hi_bf16(word) * rms_inv;
           float a0 = n0 * ns1[i], a1 = n1 * ns1[i + 1];
           bf16_round2(a0, a1);
-          float b0 = a0 * ms1[i], b1 = a1 * ms1[i + 1];
-          bf16_round2(b0, b1);
-          float c0 = b0 + shf[i], c1 = b1 + shf[i + 1];
-          bf16_round2(c0, c1);
-          v[t][i] = c0;
-          v[t][i + 1] = c1;
+          if (kMod) {
+            float b0 = a0 * ms1[i], b1 = a1 * ms1[i + 1];
+            bf16_round2(b0, b1);
+            float c0 = b0 + shf[i], c1 = b1 + shf[i + 1];
+            bf16_round2(c0, c1);
+            a0 = c0;
+            a1 = c1;
+          }
+          v[t][i] = a0;
+          v[t][i + 1] = a1;
         }
       } else if (kKind == kPlain) {
         // kernels/prepare_plain_i8.loom:89-90; stages 1 and 4 on the f16 values.
@@ -504,11 +518,17 @@ __global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArg
   // on the row being computed). Every team of the block runs the same number of
   // steps (barriers inside).
   Raw<kKind, T> other;
-  for (int base = blockIdx.x * teams; base < args.tokens; base += 2 * stride) {
-    step(cur, other);
-    if (base + stride >= args.tokens) break;
-    step(other, cur);
-  }
+  auto loop = [&](auto mod_tag) __attribute__((always_inline)) {
+    for (int base = blockIdx.x * teams; base < args.tokens; base += 2 * stride) {
+      step(cur, other, mod_tag);
+      if (base + stride >= args.tokens) break;
+      step(other, cur, mod_tag);
+    }
+  };
+  if (!kLdsFactors || modulated)
+    loop(std::true_type{});
+  else
+    loop(std::false_type{});
 }
 
 // Waves per CU the persistent grid aims for: enough to cover load latency while each

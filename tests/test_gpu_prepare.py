@@ -118,6 +118,30 @@ def test_norm_prepare_is_bit_exact_with_the_oracle(width):
     assert_same(q, s, q_ref, s_ref, width)
 
 
+@pytest.mark.parametrize("case", ["zero", "signed_zero", "one_scale", "one_shift"])
+def test_norm_prepare_with_and_without_modulation(case):
+    # With every modulation scale and shift zero (+0 or -0) the kernel skips the two
+    # identity steps; one nonzero element anywhere must bring them back. Both against
+    # the oracle, which always runs the whole formula.
+    rng = np.random.default_rng(250)
+    tokens, width = 301, 3072
+    h = bf16_bits(activations(rng, tokens, width))
+    h[5] = 0x8000  # a row of -0.0
+    ns = (rng.uniform(0.5, 1.5, width) - 1.0).astype(np.float32)
+    ms = np.zeros(width, np.float32)
+    sh = np.zeros(width, np.float32)
+    if case == "signed_zero":
+        ms[::3] = -0.0
+        sh[1::3] = -0.0
+    elif case == "one_scale":
+        ms[width - 1] = 0.25
+    elif case == "one_shift":
+        sh[17] = -0.5
+    q, s = run_norm(h, ns, ms, sh, tokens, width, width, 1e-6)
+    q_ref, s_ref = oracle.prepare_norm(h, ns, ms, sh, width, width, 1e-6)
+    assert_same(q, s, q_ref, s_ref, width)
+
+
 @pytest.mark.parametrize("width", WIDTHS)
 def test_gated_prepare_is_bit_exact_with_the_oracle(width):
     rng = np.random.default_rng(300 + width)
