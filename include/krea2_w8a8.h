@@ -202,6 +202,28 @@ int k2w8_gemm_i8_noalloc(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, cons
                          const int8_t *w, const float *scale, const float *a_scale, void *c);
 
 /*
+ * linear_norm_i8 / linear_plain_i8: one call for a projection:
+ * prepare_norm_i8 (resp. prepare_plain_i8) of h into q / q_scale, then
+ * gemm_i8 of q with w into c, as one call. Replaces the prepare -> gemm_i8 launch pair
+ * of Session::block and Quantized::forward (src/session/mod.rs:671-711,
+ * src/training/quantized.rs:66-105). The arguments are the two entry points' own (the
+ * GEMM's k_size / k_stride must equal the prepare's width / out_stride, its m is
+ * `tokens`), and the outputs are bit-identical to calling them in turn; q and q_scale
+ * are written as well. They run as the two launches. With the environment variable
+ * K2W8_LINEAR_ONE_LAUNCH=1, the wide-tile shapes (whole rounds of 256x256 or 256x192
+ * tiles, width <= 3072) run instead in one persistent launch with a grid-wide barrier
+ * between the phases (one workgroup per CU); it gives the same bits but measured
+ * slower, so it is not the default.
+ */
+int k2w8_linear_norm_i8(void *stream, const k2w8_prepare_norm_cfg *cfg, const k2w8_gemm_cfg *gemm,
+                        int64_t tokens, const void *h, const float *norm_scale,
+                        const float *mod_scale, const float *mod_shift, int8_t *q,
+                        float *q_scale, const int8_t *w, const float *scale, void *c);
+int k2w8_linear_plain_i8(void *stream, const k2w8_prepare_plain_cfg *cfg, const k2w8_gemm_cfg *gemm,
+                         int64_t tokens, const void *h, int8_t *q, float *q_scale,
+                         const int8_t *w, const float *scale, void *c);
+
+/*
  * lora_transport: replaces krea2_lora_transport (kernels/native/lora_transport.loom:5-41),
  * the 16-bit format change around the W8A8 projection of src/training/quantized.rs:66-105.
  * Each element is widened exactly to f32 and rounded (nearest even) to the other format.

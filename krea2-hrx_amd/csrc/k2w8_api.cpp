@@ -5,6 +5,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <mutex>
 #include <string>
 
@@ -207,6 +208,81 @@ int k2w8_prepare_plain_i8(void *stream, const k2w8_prepare_plain_cfg *cfg, int64
   hipError_t e = k2w8::launch_prepare(1, static_cast<hipStream_t>(stream), tokens, p);
   if (e != hipSuccess) return runtime(stage, e);
   return ok();
+}
+
+// Fused prepare -> gemm_i8: validate both halves as their own entry points do, run the
+// one-launch form where it exists for the shape, else the two launches.
+static int run_linear(const char *stage, int kind, void *stream, int64_t width, int64_t out_stride,
+                      float eps, const k2w8_gemm_cfg *gcfg, int64_t tokens, const void *h,
+                      const float *norm_scale, const float *mod_scale, const float *mod_shift,
+                      int8_t *q, float *q_scale, const int8_t *w, const float *scale, void *c) {
+  if (!gcfg) return fail(K2W8_INVALID_ARGUMENT, "%s: null configuration", stage);
+  int rc = check_prepare(stage, tokens, width, out_stride, h, q, q_scale);
+  if (rc != K2W8_OK) return rc;
+  if ((rc = check_gemm(stage, gcfg, tokens, q, w, scale, q_scale, c)) != K2W8_OK) return rc;
+  if (gcfg->k_size != width || gcfg->k_stride != out_stride)
+    return fail(K2W8_INVALID_ARGUMENT,
+                "%s: the GEMM's k_size and k_stride must be the prepare's width and out_stride", stage);
+  if (kind == 0) {
+    if (!norm_scale || !mod_scale || !mod_shift)
+      return fail(K2W8_INVALID_ARGUMENT, "%s: null norm or modulation vector", stage);
+    if (!aligned(norm_scale, 16) || !aligned(mod_scale, 16) || !aligned(mod_shift, 16))
+      return fail(K2W8_INVALID_ARGUMENT, "%s: norm and modulation vectors must be 16-byte aligned", stage);
+    if (!(eps >= 0.0f)) return fail(K2W8_INVALID_ARGUMENT, "%s: eps must be >= 0", stage);
+  }
+  if ((rc = ensure_configured(stage)) != K2W8_OK) return rc;
+  k2w8::PrepareLaunch p;
+  p.h = h;
+  p.norm_scale = norm_scale;
+  p.mod_scale = mod_scale;
+  p.mod_shift = mod_shift;
+  p.q = q;
+  p.q_scale = q_scale;
+  p.width = width;
+  p.out_stride = out_stride;
+  p.eps = eps;
+  k2w8::GemmLaunch l;
+  l.a = q;
+  l.w = w;
+  l.w_scale = scale;
+  l.a_scale = q_scale;
+  l.c = c;
+  l.m = tokens;
+  l.n = gcfg->n_size;
+  l.k = gcfg->k_size;
+  l.lda = gcfg->k_stride;
+  l.m_group = (int)gcfg->m_group;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // Two launches by default: the one-launch form measured slower (configs[1] 135 ->
+  // 148 us: its prepare phase runs at one workgroup per CU, and the grid barrier's
+  // agent-scope release and acquire write back and invalidate each XCD's L2). Setting
+  // K2W8_LINEAR_ONE_LAUNCH=1 selects it (read on every call).
+  const char *one = getenv("K2W8_LINEAR_ONE_LAUNCH");
+  hipError_t e = (one && one[0] == '1') ? k2w8::launch_prepare_gemm(kind, s, tokens, p, l)
+                                        : hipErrorNotSupported;
+  if (e == hipErrorNotSupported) {
+    e = k2w8::launch_prepare(kind, s, tokens, p);
+    if (e == hipSuccess) e = k2w8::launch_gemm(k2w8::kEpiPlain, s, l);
+  }
+  if (e != hipSuccess) return runtime(stage, e);
+  return ok();
+}
+
+int k2w8_linear_norm_i8(void *stream, const k2w8_prepare_norm_cfg *cfg, const k2w8_gemm_cfg *gemm,
+                        int64_t tokens, const void *h, const float *norm_scale,
+                        const float *mod_scale, const float *mod_shift, int8_t *q,
+                        float *q_scale, const int8_t *w, const float *scale, void *c) {
+  if (!cfg) return fail(K2W8_INVALID_ARGUMENT, "linear_norm_i8: null configuration");
+  return run_linear("linear_norm_i8", 0, stream, cfg->width, cfg->out_stride, cfg->eps, gemm,
+                    tokens, h, norm_scale, mod_scale, mod_shift, q, q_scale, w, scale, c);
+}
+
+int k2w8_linear_plain_i8(void *stream, const k2w8_prepare_plain_cfg *cfg, const k2w8_gemm_cfg *gemm,
+                         int64_t tokens, const void *h, int8_t *q, float *q_scale,
+                         const int8_t *w, const float *scale, void *c) {
+  if (!cfg) return fail(K2W8_INVALID_ARGUMENT, "linear_plain_i8: null configuration");
+  return run_linear("linear_plain_i8", 1, stream, cfg->width, cfg->out_stride, 0.0f, gemm, tokens,
+                    h, nullptr, nullptr, nullptr, q, q_scale, w, scale, c);
 }
 
 int k2w8_prepare_gated_i8(void *stream, const k2w8_prepare_gated_cfg *cfg, int64_t tokens,

@@ -277,8 +277,11 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs &g, v16i (&acc)[FM
   }
 }
 
+// One output tile (workgroup number `bid` of the tile order) through the K loop and
+// the epilogue: the body of gemm_kernel, callable from a persistent kernel. `smem` is
+// the workgroup's dynamic LDS.
 template <int BM, int BN, int WM, int WN, int BK, int STAGES, int EPI>
-__global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
+__device__ __forceinline__ void gemm_tile(const GemmArgs &g, int bid, uint8_t *smem) {
   constexpr int kWaves = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;  // wave sub-tile
   constexpr int FM = WTM / 32, FN = WTN / 32;  // 32x32 blocks per wave
@@ -290,14 +293,13 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
   constexpr int kIns = kAIns + kBIns;
   static_assert(kAIns * kWaves * 1024 == BM * BK && kBIns * kWaves * 1024 == BN * BK, "staging");
   static_assert(BK % 32 == 0 && STAGES >= 2 && kWaves % 2 == 0, "pipeline");
-  extern __shared__ __align__(16) uint8_t smem[];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
   int tm, tn;
-  tile_of(blockIdx.x, (g.m + BM - 1) / BM, g.n / BN, g.m_group, tm, tn);
+  tile_of(bid, (g.m + BM - 1) / BM, g.n / BN, g.m_group, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
 
   // Transfers. The stage's A rows are 1 KiB blocks, block b = v*kAIns + i for "virtual
@@ -466,6 +468,12 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
   } else {  // int32 output of the 256x256 tile: 135 KiB would not fit; direct stores
     store_tile<EPI, FM, FN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, fr, kh);
   }
+}
+
+template <int BM, int BN, int WM, int WN, int BK, int STAGES, int EPI>
+__global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  gemm_tile<BM, BN, WM, WN, BK, STAGES, EPI>(g, blockIdx.x, smem);
 }
 
 template <int BM, int BN, int WM, int WN, int BK, int STAGES>

@@ -48,6 +48,11 @@ struct GemmLaunch {
 };
 
 hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &g);
+// prepare_norm_i8 (kind 0) or prepare_plain_i8 (kind 1) and gemm_i8 in one persistent
+// launch (the wide-tile shapes whose tiles fill whole rounds, prepare width <= 3072);
+// hipErrorNotSupported otherwise, having launched nothing.
+hipError_t launch_prepare_gemm(int kind, hipStream_t stream, int64_t tokens, const PrepareLaunch &p,
+                               const GemmLaunch &g);
 // Few-token kernel (any m; chosen by launch_gemm for small m).
 bool skinny_streams(int epilogue, const GemmLaunch &g);
 hipError_t launch_skinny(int epilogue, hipStream_t stream, const GemmLaunch &g);

@@ -160,7 +160,7 @@ __device__ __align__(16) uint16_t g_sigmoid_bf16[65536];
 constexpr size_t kSigmoidTableBytes = sizeof(uint16_t) * 65536;
 constexpr int kGatedWaves = 16;  // waves per gated block: one block per CU (the table)
 
-__global__ __launch_bounds__(256) void sigmoid_table_kernel() {
+[[maybe_unused]] __global__ __launch_bounds__(256) void sigmoid_table_kernel() {
   const int b = blockIdx.x * 256 + threadIdx.x;
   const float s = bf16_round1(sigmoid(f16_value((uint16_t)b)));
   g_sigmoid_bf16[b] = (uint16_t)(__float_as_uint(s) >> 16);
@@ -187,8 +187,12 @@ struct Bounds {
 
 // kSingle: one-wave teams (no block barriers, the norm's sum of squares from
 // registers, norm factors staged in LDS). Otherwise teams of wpt waves.
+// The prepare of the rows a block's teams own (block `block` of `blocks`): the body of
+// prepare_kernel, callable from a fused kernel's producer phase. `factor_lds` is the
+// block's dynamic LDS (norm factors or the sigmoid table).
 template <int kKind, int T, bool kSingle>
-__global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArgs args) {
+__device__ __forceinline__ void prepare_rows(const PrepareArgs &args, int block, int blocks,
+                                             float4 *factor_lds) {
   constexpr bool kQuarter = (kKind == kPlain);
   __shared__ float lds_part[2][kMaxTeams][8];         // norm partials (multi-wave teams)
   __shared__ float lds_amax[2][kMaxTeams][kMaxWpt];   // wave maxima (multi-wave teams)
@@ -226,10 +230,10 @@ __global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArg
     }
   };
 
-  const int stride = gridDim.x * teams;
+  const int stride = blocks * teams;
   int iter = 0;
   Raw<kKind, T> cur;
-  int token = blockIdx.x * teams + team;
+  int token = block * teams + team;
   load(cur, token);
 
   // Norm vectors (kernels/prepare_norm_i8.loom:150-158) as the per-element factors
@@ -238,7 +242,6 @@ __global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArg
   // the 208-byte run stride puts 16 consecutive runs on 16 distinct bank groups, so
   // the lanes' 16-byte reads do not conflict; a 192-byte stride repeats every 4 runs),
   // wider teams read them from global memory per token.
-  extern __shared__ float4 factor_lds[];
   constexpr bool kLdsFactors = (kKind == kNorm) && kSingle;
   if (kKind == kGated) {
     const uint4 *src = reinterpret_cast<const uint4 *>(g_sigmoid_bf16);
@@ -519,7 +522,7 @@ __global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArg
   // steps (barriers inside).
   Raw<kKind, T> other;
   auto loop = [&](auto mod_tag) __attribute__((always_inline)) {
-    for (int base = blockIdx.x * teams; base < args.tokens; base += 2 * stride) {
+    for (int base = block * teams; base < args.tokens; base += 2 * stride) {
       step(cur, other, mod_tag);
       if (base + stride >= args.tokens) break;
       step(other, cur, mod_tag);
@@ -531,6 +534,13 @@ __global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArg
     loop(std::false_type{});
 }
 
+template <int kKind, int T, bool kSingle>
+__global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArgs args) {
+  extern __shared__ float4 factor_lds[];
+  prepare_rows<kKind, T, kSingle>(args, blockIdx.x, gridDim.x, factor_lds);
+}
+
+#ifndef K2W8_PREPARE_NO_ENTRY
 // Waves per CU the persistent grid aims for: enough to cover load latency while each
 // team still loops over several tokens. The norm prepare's one-wave teams do better
 // with fewer, longer-lived waves, whose prefetch of the next row overlaps the current
@@ -608,7 +618,9 @@ hipError_t launch_kind(hipStream_t stream, PrepareArgs a) {
   return launch_t<kKind, false>(t, stream, a);
 }
 
+#endif  // K2W8_PREPARE_NO_ENTRY
 }  // namespace
+#ifndef K2W8_PREPARE_NO_ENTRY
 
 hipError_t launch_prepare(int kind, hipStream_t stream, int64_t tokens, const PrepareLaunch &p) {
   PrepareArgs a;
@@ -674,5 +686,7 @@ hipError_t prepare_gated_ready(hipStream_t stream) {
   if (e == hipSuccess) ready[dev] = true;
   return e;
 }
+
+#endif  // K2W8_PREPARE_NO_ENTRY
 
 }  // namespace k2w8

@@ -26,6 +26,8 @@ from .ops import (  # noqa: F401
     gemm_i8_swiglu,
     gemm_set_workspace,
     gemm_workspace_bytes,
+    linear_norm_i8,
+    linear_plain_i8,
     lora_transport,
     sigmoid_f32,
     prepare_gated_i8,
@@ -52,6 +54,8 @@ __all__ = [
     "gemm_set_workspace",
     "gemm_workspace_bytes",
     "lib",
+    "linear_norm_i8",
+    "linear_plain_i8",
     "library_path",
     "lora_transport",
     "sigmoid_f32",

@@ -189,6 +189,47 @@ def gemm_i8_acc(a, w, acc, *, cfg: GemmConfig, m=None, stream=None):
     check(lib().k2w8_gemm_i8_acc(_stream(stream), ctypes.byref(k), m, pa, pw, out))
 
 
+def linear_norm_i8(h, norm_scale, mod_scale, mod_shift, q, q_scale, w, scale, c, *,
+                   cfg: "GemmConfig", eps, tokens=None, stream=None):
+    """prepare_norm_i8 of ``h`` into ``q``/``q_scale``, then gemm_i8 of ``q`` with ``w``
+    into ``c``, as one call (one persistent launch for the wide-tile shapes). The
+    prepare's width and out_stride are the GEMM config's k_size and k_stride."""
+    n = _tokens(h, tokens)
+    width, out_stride = cfg.k_size, cfg.k_stride
+    pc = PrepareNormCfg(width, out_stride, eps)
+    args = (
+        _buf(h, "h", torch.bfloat16, n * width),
+        _buf(norm_scale, "norm_scale", torch.float32, width),
+        _buf(mod_scale, "mod_scale", torch.float32, width),
+        _buf(mod_shift, "mod_shift", torch.float32, width),
+        _buf(q, "q", torch.int8, (n - 1) * out_stride + width),
+        _buf(q_scale, "q_scale", torch.float32, n),
+        _buf(w, "w", torch.int8, (cfg.n_size - 1) * cfg.k_stride + cfg.k_size),
+        _buf(scale, "scale", torch.float32, cfg.n_size),
+        _buf(c, "c", torch.float16, n * cfg.n_size),
+    )
+    k = cfg.c()
+    check(lib().k2w8_linear_norm_i8(_stream(stream), ctypes.byref(pc), ctypes.byref(k), n, *args))
+
+
+def linear_plain_i8(h, q, q_scale, w, scale, c, *, cfg: "GemmConfig", tokens=None, stream=None):
+    """prepare_plain_i8 of f16 ``h`` into ``q``/``q_scale``, then gemm_i8 into ``c``, as
+    one call (one persistent launch for the wide-tile shapes)."""
+    n = _tokens(h, tokens)
+    width, out_stride = cfg.k_size, cfg.k_stride
+    pc = PreparePlainCfg(width, out_stride)
+    args = (
+        _buf(h, "h", torch.float16, n * width),
+        _buf(q, "q", torch.int8, (n - 1) * out_stride + width),
+        _buf(q_scale, "q_scale", torch.float32, n),
+        _buf(w, "w", torch.int8, (cfg.n_size - 1) * cfg.k_stride + cfg.k_size),
+        _buf(scale, "scale", torch.float32, cfg.n_size),
+        _buf(c, "c", torch.float16, n * cfg.n_size),
+    )
+    k = cfg.c()
+    check(lib().k2w8_linear_plain_i8(_stream(stream), ctypes.byref(pc), ctypes.byref(k), n, *args))
+
+
 def gemm_set_workspace(workspace, *, stream=None):
     """Hand the GEMMs on ``stream`` (default: torch's current stream) a caller-owned
     split-K workspace (a device tensor; its bytes are used, its dtype is not), or remove

@@ -1,0 +1,112 @@
+"""The fused prepare -> GEMM entry points (k2w8_linear_norm_i8, k2w8_linear_plain_i8):
+bit-identical to the two entry points called in turn (q, q_scale and the output), in
+the one-launch form (K2W8_LINEAR_ONE_LAUNCH=1: whole rounds of 256x256 or 256x192
+tiles in one persistent kernel) and in the default two-launch form; the one-launch
+kernel's grid barrier leaves its counters at zero, so back-to-back calls and graph
+replays give the same results."""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_common import activations, bf16_bits, channel_scales, dev, f16_bits, host, int8_weights, k2
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(params=["one_launch", "two_launches"])
+def mode(request, monkeypatch):
+    monkeypatch.setenv("K2W8_LINEAR_ONE_LAUNCH", "1" if request.param == "one_launch" else "0")
+    assert os.environ["K2W8_LINEAR_ONE_LAUNCH"] in ("0", "1")
+    return request.param
+
+
+def case(kind, m, k, n, seed):
+    rng = np.random.default_rng(seed)
+    x = activations(rng, m, k)
+    h = bf16_bits(x) if kind == "norm" else f16_bits(x)
+    w = int8_weights(rng, n, k)
+    ws = channel_scales(rng, n)
+    ns = (rng.uniform(0.5, 1.5, k) - 1.0).astype(np.float32)
+    zero = np.zeros(k, np.float32)
+    dtype = torch.bfloat16 if kind == "norm" else torch.float16
+    return dict(kind=kind, m=m, k=k, n=n, h=dev(h, dtype), h_bits=h, w=dev(w), ws=dev(ws),
+                ns=dev(ns), zero=dev(zero), ns_np=ns, zero_np=zero)
+
+
+def run(c, fused, out=None, q=None, s=None):
+    m, k, n = c["m"], c["k"], c["n"]
+    q = torch.full((m, k), 91, dtype=torch.int8, device="cuda") if q is None else q
+    s = torch.zeros(m, dtype=torch.float32, device="cuda") if s is None else s
+    out = torch.zeros((m, n), dtype=torch.float16, device="cuda") if out is None else out
+    cfg = k2.GemmConfig(k_size=k, n_size=n, k_stride=k)
+    if fused and c["kind"] == "norm":
+        k2.linear_norm_i8(c["h"], c["ns"], c["zero"], c["zero"], q, s, c["w"], c["ws"], out, cfg=cfg,
+                          eps=1e-6)
+    elif fused:
+        k2.linear_plain_i8(c["h"], q, s, c["w"], c["ws"], out, cfg=cfg)
+    elif c["kind"] == "norm":
+        k2.prepare_norm_i8(c["h"], c["ns"], c["zero"], c["zero"], q, s, width=k, out_stride=k, eps=1e-6)
+        k2.gemm_i8(q, c["w"], c["ws"], s, out, cfg=cfg)
+    else:
+        k2.prepare_plain_i8(c["h"], q, s, width=k, out_stride=k)
+        k2.gemm_i8(q, c["w"], c["ws"], s, out, cfg=cfg)
+    return q, s, out
+
+
+SHAPES = [
+    ("plain", 4096, 3072, 12288),  # north star: 768 tiles of 256x256, one launch
+    ("norm", 4096, 3072, 9216),    # configs[1]: 768 tiles of 256x192, one launch
+    ("norm", 2048, 2048, 8192),    # 256 tiles of 256x256 (one round), width 2048
+    ("norm", 4544, 3072, 9216),    # ragged rounds: the two-launch fallback
+    ("plain", 300, 1024, 1024),    # mid-M: the two-launch fallback
+]
+
+
+@pytest.mark.parametrize("kind,m,k,n", SHAPES)
+def test_fused_equals_the_two_entry_points(kind, m, k, n, mode):
+    c = case(kind, m, k, n, seed=m + k + n)
+    q1, s1, o1 = run(c, fused=True)
+    q2, s2, o2 = run(c, fused=False)
+    torch.cuda.synchronize()
+    assert torch.equal(q1, q2) and torch.equal(s1, s2)
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+    # and the prepared rows against the oracle (the GEMM halves are pinned elsewhere)
+    rows = np.arange(0, m, max(1, m // 16))
+    if kind == "norm":
+        q_ref, s_ref = oracle.prepare_norm(c["h_bits"][rows], c["ns_np"], c["zero_np"], c["zero_np"],
+                                           k, k, 1e-6)
+    else:
+        q_ref, s_ref = oracle.prepare_plain(c["h_bits"][rows], k, k)
+    assert np.array_equal(host(q1)[rows], q_ref) and np.array_equal(host(s1)[rows], s_ref)
+
+
+def test_back_to_back_calls_and_graph_replays(mode):
+    c = case("norm", 4096, 3072, 9216, seed=5)
+    q, s, want = run(c, fused=False)
+    torch.cuda.synchronize()
+    out = torch.zeros_like(want)
+    for _ in range(3):  # eager, back to back: the barrier's counters return to zero
+        run(c, fused=True, out=out)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    qg = torch.zeros_like(q)
+    sg = torch.zeros_like(s)
+    og = torch.zeros_like(want)
+    run(c, fused=True, out=og, q=qg, s=sg)  # one-time set-up outside the capture
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        run(c, fused=True, out=og, q=qg, s=sg)
+    for replay in range(3):
+        og.zero_()
+        qg.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(og.view(torch.int16), want.view(torch.int16)), replay
+        assert torch.equal(qg, q), replay
