@@ -26,10 +26,15 @@ namespace k2w8 {
 namespace gemm {
 
 typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));
+// Buffer descriptor word 3 for raw 32-bit buffer access on CDNA (no swizzle, no format
+// conversion), and the cache-policy operand bit of a store's sc1 (system coherence scope:
+// the L2 writes the data through).
+constexpr int kBufferWord3 = 0x00020000;
+constexpr int kCachePolicySc1 = 16;
 
 // Epilogue of one wave's (32 FM) x (32 FN) sub-tile at rows m_base.., columns n_base..
 template <int EPI, int FM, int FN>
-__device__ __forceinline__ void store_tile(const GemmArgs &g, v16i (&acc)[FM][FN], int m_base,
+__device__ __forceinline__ void store_tile(const GemmArgs &g, int split, v16i (&acc)[FM][FN], int m_base,
                                            int n_base, int fr, int kh) {
   // The MFMAs run with the weights as their row operand, so block (i, j) holds C^T:
   // lane (fr, kh) owns token m = m_base + 32i + fr and, in register e, channel
@@ -107,7 +112,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, v16i (&acc)[FM][FN
     for (int i = 0; i < FM; ++i) {
       if (!live[i]) continue;
       if (EPI == kEpiAcc) {
-        int32_t *out = static_cast<int32_t *>(g.c) + (int64_t)blockIdx.y * g.split_stride +
+        int32_t *out = static_cast<int32_t *>(g.c) + (int64_t)split * g.split_stride +
                        m_row[i] * g.ldc + nb;
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -159,21 +164,67 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, v16i (&acc)[FM][FN
 // the staged value is bf16(v); x = bf16(x + bf16(gate * v)).
 // `region` holds 32 rows of kPitch bytes (the output columns plus 16 bytes, which
 // spreads the rows' 8-byte writes over the banks).
-template <int EPI, int FM, int FN>
-__device__ __forceinline__ void store_tile_lds(const GemmArgs &g, v16i (&acc)[FM][FN], int m_base,
-                                               int n_base, int fr, int kh, int lane,
-                                               uint8_t *region) {
+// Per-tile epilogue operands, staged into LDS after the K loop's stages by one wave's
+// transfers at the start of the tile (so their latency hides behind the K loop instead
+// of stalling the epilogue): the BN channel scales, then BN per-channel extras (the f16
+// bias, or the residual's f32 gate), then the BM row scales (ghost rows repeat the last).
+template <int BM, int BN>
+struct EpiOperands {
+  static constexpr int kWs = 0, kExtra = BN * 4, kAs = BN * 8;
+  static constexpr int kBytes = BN * 8 + BM * 4;
+};
+
+template <int EPI, int BM, int BN>
+__device__ __forceinline__ void stage_epi_operands(const GemmArgs &g, int m0, int n0, int lane,
+                                                   uint32_t lds) {
+  using E = EpiOperands<BM, BN>;
+  static_assert(BN * 4 <= 1024 && BM % 64 == 0 || BM < 64, "one transfer per column operand");
+  if (EPI == kEpiAcc) return;
+  if (lane < BN / 4) dma16(lds + E::kWs, reinterpret_cast<const int8_t *>(g.w_scale), (uint32_t)(n0 * 4 + lane * 16));
+  if (EPI == kEpiBias && lane < BN / 8)
+    dma16(lds + E::kExtra, reinterpret_cast<const int8_t *>(g.bias), (uint32_t)(n0 * 2 + lane * 16));
+  if (EPI == kEpiResid && lane < BN / 4)
+    dma16(lds + E::kExtra, reinterpret_cast<const int8_t *>(g.gate), (uint32_t)(n0 * 4 + lane * 16));
+#pragma unroll
+  for (int r = 0; r < BM; r += 64) {
+    const int m = min(m0 + r + lane, g.m - 1);
+    if (BM >= 64 || lane < BM) dma4(lds + E::kAs + r * 4, g.a_scale, (uint32_t)(m * 4));
+  }
+}
+
+// Epilogue through LDS (every output but split-K's int32 slices, which also go through
+// it: 4-byte elements). The
+// f32 arithmetic up to the stored value's rounding runs on the accumulator layout,
+// as in store_tile; the packed 16-bit values then go to this wave's LDS region, one
+// 32-row block at a time, and come back as 16-byte runs of eight consecutive output
+// columns of one row, so every global store writes whole row segments (a store
+// instruction covers 64 x 16 bytes) instead of 32 rows x 16 bytes. The residual's
+// read-modify-write of x happens on that row layout, with the same f32 operations:
+// the staged value is bf16(v); x = bf16(x + bf16(gate * v)).
+// `region` holds 32 rows of kPitch bytes (the output columns plus 16 bytes, which
+// spreads the rows' 8-byte writes over the banks). `ops` is the tile's staged
+// epilogue operands (EpiOperands), `m_off`/`n_off` this wave's offsets in the tile.
+// The block's LDS reads (and the residual's reads of x) are all issued before the
+// first store, so the block waits one round trip for them, not one per row run.
+template <int EPI, int FM, int FN, int BM, int BN>
+__device__ __forceinline__ void store_tile_lds(const GemmArgs &g, int split, v16i (&acc)[FM][FN], int m0,
+                                               int n0, int m_off, int n_off, int fr, int kh, int lane,
+                                               uint8_t *region, const uint8_t *ops) {
+  using E = EpiOperands<BM, BN>;
   constexpr int kCols = EPI == kEpiSwiglu ? 16 * FN : 32 * FN;  // output columns
   constexpr int kElem = EPI == kEpiAcc ? 4 : 2;                  // output bytes
   constexpr int kPitch = kCols * kElem + 16;
   constexpr int kChunks = kCols * kElem / 16;  // 16-byte runs per row
   constexpr int kReads = (32 * kChunks + 63) / 64;
+  const int m_base = m0 + m_off, n_base = n0 + n_off;
   const int out_base = EPI == kEpiSwiglu ? n_base / 2 : n_base;
+  const float *ws_lds = reinterpret_cast<const float *>(ops + E::kWs) + n_off;
+  const float *as_lds = reinterpret_cast<const float *>(ops + E::kAs) + m_off;
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
-    const int m = m_base + i * 32 + fr;
-    const float as = EPI == kEpiAcc ? 1.0f : g.a_scale[m < g.m ? m : g.m - 1];
+    const float as = EPI == kEpiAcc ? 1.0f : as_lds[i * 32 + fr];
     uint8_t *row = region + fr * kPitch;
+    float sw_g[EPI == kEpiSwiglu ? FN * 8 : 2], sw_u[EPI == kEpiSwiglu ? FN * 8 : 2];
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       if (EPI == kEpiAcc) {
@@ -186,38 +237,33 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs &g, v16i (&acc)[FM
       // Per-channel vectors of this lane's channels: n = n_base + 32j + 8q + 4kh + r
       // (SwiGLU: registers 8-15 are the up channels, 16 further on).
       float ws[16], extra[16];
-      const int nb = n_base + j * 32 + kh * 4;
+      const int nb = j * 32 + kh * 4;  // within the wave's columns
 #pragma unroll
       for (int q = 0; q < 4 && EPI != kEpiAcc; ++q) {
         const int ch = (EPI == kEpiSwiglu && q >= 2) ? nb + 16 + 8 * (q - 2) : nb + 8 * q;
-        const float4 v = *reinterpret_cast<const float4 *>(g.w_scale + ch);
+        const float4 v = *reinterpret_cast<const float4 *>(ws_lds + ch);
         ws[4 * q] = v.x; ws[4 * q + 1] = v.y; ws[4 * q + 2] = v.z; ws[4 * q + 3] = v.w;
         if (EPI == kEpiBias) {
-          const uint2 b = *reinterpret_cast<const uint2 *>(g.bias + ch);
+          const uint2 b = *reinterpret_cast<const uint2 *>(ops + E::kExtra + 2 * (n_off + ch));
           extra[4 * q] = f16_value(b.x & 0xffffu); extra[4 * q + 1] = f16_value(b.x >> 16);
           extra[4 * q + 2] = f16_value(b.y & 0xffffu); extra[4 * q + 3] = f16_value(b.y >> 16);
         }
       }
       if (EPI == kEpiSwiglu) {
-        // registers 0-7: gate channels 8q+4kh+r (q<2), 8-15: the matching ups
+        // registers 0-7: gate channels 8q+4kh+r (q<2), 8-15: the matching ups; the
+        // products of the block's FN x 8 pairs are formed together (swiglu_products)
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          uint32_t packed[2];
-#pragma unroll
-          for (int r = 0; r < 4; r += 2) {
-            float g0 = ((float)acc[i][j][4 * q + r] * ws[4 * q + r]) * as;
-            float g1 = ((float)acc[i][j][4 * q + r + 1] * ws[4 * q + r + 1]) * as;
-            float u0 = ((float)acc[i][j][8 + 4 * q + r] * ws[8 + 4 * q + r]) * as;
-            float u1 = ((float)acc[i][j][8 + 4 * q + r + 1] * ws[8 + 4 * q + r + 1]) * as;
-            bf16_round2(g0, g1);
-            bf16_round2(u0, u1);
-            float s0 = g0 * sigmoid(g0), s1 = g1 * sigmoid(g1);
-            bf16_round2(s0, s1);
-            float p0 = s0 * u0, p1 = s1 * u1;
-            bf16_round2(p0, p1);
-            packed[r >> 1] = f16_pack2(p0, p1);
-          }
-          *reinterpret_cast<uint2 *>(row + 2 * (j * 16 + 8 * q + 4 * kh)) = make_uint2(packed[0], packed[1]);
+        for (int e = 0; e < 8; e += 2) {
+          float g0 = ((float)acc[i][j][e] * ws[e]) * as;
+          float g1 = ((float)acc[i][j][e + 1] * ws[e + 1]) * as;
+          float u0 = ((float)acc[i][j][8 + e] * ws[8 + e]) * as;
+          float u1 = ((float)acc[i][j][8 + e + 1] * ws[8 + e + 1]) * as;
+          bf16_round2(g0, g1);
+          bf16_round2(u0, u1);
+          sw_g[j * 8 + e] = g0;
+          sw_g[j * 8 + e + 1] = g1;
+          sw_u[j * 8 + e] = u0;
+          sw_u[j * 8 + e + 1] = u1;
         }
         continue;
       }
@@ -243,33 +289,72 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs &g, v16i (&acc)[FM
         *reinterpret_cast<uint2 *>(row + 2 * (j * 32 + 8 * q + 4 * kh)) = make_uint2(packed[0], packed[1]);
       }
     }
-    // This wave's own LDS writes, read back in row order (LDS serves one wave in order).
+    if constexpr (EPI == kEpiSwiglu) {
+      swiglu_products(sw_g, sw_u);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+          *reinterpret_cast<uint2 *>(row + 2 * (j * 16 + 8 * q + 4 * kh)) =
+              make_uint2(f16_pack2(sw_g[j * 8 + 4 * q], sw_g[j * 8 + 4 * q + 1]),
+                         f16_pack2(sw_g[j * 8 + 4 * q + 2], sw_g[j * 8 + 4 * q + 3]));
+    }
+    // This wave's own LDS writes, read back in row order (LDS serves one wave in order):
+    // first every read of the block, then the stores.
+    v4u_t vals[kReads];
+#pragma unroll
+    for (int s = 0; s < kReads; ++s) {
+      const int idx = s * 64 + lane;
+      const int r = min(idx / kChunks, 31), c = idx - (idx / kChunks) * kChunks;
+      vals[s] = *reinterpret_cast<const v4u_t *>(region + r * kPitch + 16 * c);
+    }
+    v4u_t prior[EPI == kEpiResid ? kReads : 1];
+    if (EPI == kEpiResid) {
+#pragma unroll
+      for (int s = 0; s < kReads; ++s) {
+        const int idx = s * 64 + lane;
+        const int r = idx / kChunks, c = idx - r * kChunks;
+        const int tok = min(m_base + i * 32 + min(r, 31), g.m - 1);
+        prior[s] = *reinterpret_cast<const v4u_t *>(static_cast<const uint16_t *>(g.c) + (int64_t)tok * g.ldc +
+                                                    out_base + 8 * c);
+      }
+    }
 #pragma unroll
     for (int s = 0; s < kReads; ++s) {
       const int idx = s * 64 + lane;
       const int r = idx / kChunks, c = idx - r * kChunks;
       const int tok = m_base + i * 32 + r;
       if (r >= 32 || tok >= g.m) continue;
-      v4u_t v = *reinterpret_cast<const v4u_t *>(region + r * kPitch + 16 * c);
+      v4u_t v = vals[s];
       if (EPI == kEpiAcc) {
-        int32_t *out = static_cast<int32_t *>(g.c) + (int64_t)blockIdx.y * g.split_stride +
-                       (int64_t)tok * g.ldc + n_base + 4 * c;
-        *reinterpret_cast<v4u_t *>(out) = v;
+        const int64_t at = (int64_t)tok * g.ldc + n_base + 4 * c;
+        if (g.k_split_steps > 0) {
+          // Split-K partial sums are written through to memory (sc1): the kernel's end
+          // then has no dirty L2 lines of them to write back before the reduction kernel
+          // can start (measured: 3.0 -> 1.3 us between the two at 16 MB of partials).
+          // The host keeps a slice below 2 GiB, so the 32-bit buffer offset holds it.
+          int32_t *slice = static_cast<int32_t *>(g.c) + (int64_t)split * g.split_stride;
+          const __amdgpu_buffer_rsrc_t rsrc =
+              __builtin_amdgcn_make_buffer_rsrc(slice, (short)0, 0x7fffffff, kBufferWord3);
+          __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, (int)(at * 4), 0, kCachePolicySc1);
+        } else {
+          *reinterpret_cast<v4u_t *>(static_cast<int32_t *>(g.c) + at) = v;
+        }
         continue;
       }
       uint16_t *out = static_cast<uint16_t *>(g.c) + (int64_t)tok * g.ldc + out_base + 8 * c;
       if (EPI == kEpiResid) {
-        const v4u_t prior = *reinterpret_cast<const v4u_t *>(out);
-        const float4 g0 = *reinterpret_cast<const float4 *>(g.gate + n_base + 8 * c);
-        const float4 g1 = *reinterpret_cast<const float4 *>(g.gate + n_base + 8 * c + 4);
+        const float *gate = reinterpret_cast<const float *>(ops + E::kExtra) + n_off + 8 * c;
+        const float4 g0 = *reinterpret_cast<const float4 *>(gate);
+        const float4 g1 = *reinterpret_cast<const float4 *>(gate + 4);
         const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
           float a0 = __uint_as_float(v[w] << 16) * gv[2 * w];
           float a1 = __uint_as_float(v[w] & 0xffff0000u) * gv[2 * w + 1];
           bf16_round2(a0, a1);
-          v[w] = bf16_pack2(__uint_as_float(prior[w] << 16) + a0,
-                            __uint_as_float(prior[w] & 0xffff0000u) + a1);
+          v[w] = bf16_pack2(__uint_as_float(prior[s][w] << 16) + a0,
+                            __uint_as_float(prior[s][w] & 0xffff0000u) + a1);
         }
       }
       *reinterpret_cast<v4u_t *>(out) = v;
@@ -280,9 +365,16 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs &g, v16i (&acc)[FM
 // One output tile (workgroup number `bid` of the tile order) through the K loop and
 // the epilogue: the body of gemm_kernel, callable from a persistent kernel. `smem` is
 // the workgroup's dynamic LDS.
-template <int BM, int BN, int WM, int WN, int BK, int STAGES, int EPI>
+//
+// KG > 1 puts KG groups of WM x WN waves on the tile, group k taking the k-th part of
+// every K step's 32-byte slices; after the K loop the other groups' sums are added to
+// group 0's through LDS (integer addition, exact) and group 0 runs the epilogue. On a
+// small tile (64x64 with one workgroup per CU) that gives each SIMD a second wave, so
+// the MFMAs of one overlap the transfer issue of the other.
+template <int BM, int BN, int WM, int WN, int BK, int STAGES, int EPI, int KG = 1>
 __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int bid, uint8_t *smem) {
-  constexpr int kWaves = WM * WN;
+  constexpr int kCw = WM * WN;      // waves of one K group
+  constexpr int kWaves = kCw * KG;  // waves of the workgroup
   constexpr int WTM = BM / WM, WTN = BN / WN;  // wave sub-tile
   constexpr int FM = WTM / 32, FN = WTN / 32;  // 32x32 blocks per wave
   constexpr int kCpr = BK / 16;                // 16-byte chunks per staged row
@@ -298,8 +390,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int bid, uint8_t *s
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  int tm, tn;
-  tile_of(bid, (g.m + BM - 1) / BM, g.n / BN, g.m_group, tm, tn);
+  int tm, tn, split = 0;
+  if (g.k_split_steps > 0)
+    split_tile_of(bid, blockIdx.y, gridDim.x, gridDim.y, (g.m + BM - 1) / BM, tm, tn, split);
+  else
+    tile_of(bid, (g.m + BM - 1) / BM, g.n / BN, g.m_group, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
 
   // Transfers. The stage's A rows are 1 KiB blocks, block b = v*kAIns + i for "virtual
@@ -321,7 +416,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int bid, uint8_t *s
   // This workgroup's K steps (all of K, or its split's share).
   int kt_count = g.k / BK, kt_first = 0;
   if (g.k_split_steps > 0) {
-    kt_first = (int)blockIdx.y * g.k_split_steps;
+    kt_first = split * g.k_split_steps;
     kt_count = min(g.k_split_steps, kt_count - kt_first);
   }
   const uint32_t k_first = (uint32_t)(kt_first * BK);
@@ -359,6 +454,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int bid, uint8_t *s
       for (int i = 0; i < kBIns; ++i)
         dma16(b_lds + so + (j * kHalf * kBIns + i) * 1024, g.w, b_off[j * kBIns + i] + ko);
   };
+  // The epilogue's operands first: a transfer that is older than every stage's is done
+  // once any wait for a stage is.
+  const uint32_t ops_lds = lds0 + STAGES * kStage;
+  if (wave == 0) stage_epi_operands<EPI, BM, BN>(g, m0, n0, lane, ops_lds);
 #pragma unroll
   for (int s = 0; s < STAGES; ++s)
     if (s < kt_count) issue(s);
@@ -376,7 +475,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int bid, uint8_t *s
   asm volatile("; agpr hint %0" ::"a"(0));
 #endif
 
-  const int wm = wave / WN, wn = wave % WN;
+  const int kg = wave / kCw, cw = wave - kg * kCw;
+  const int wm = cw / WN, wn = cw % WN;
   const int fr = lane & 31, kh = lane >> 5;
   // Per-lane LDS byte offsets of this wave's fragment rows (chunk added per K slice;
   // a lane's fragment rows differ by multiples of 32 and share the swizzle key).
@@ -395,14 +495,15 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int bid, uint8_t *s
   // for the next stage have landed and nobody reads the current stage any more, so
   // the transfer for stage kt+STAGES can refill it. Barrier and first reads hide
   // behind the last slice's MFMAs.
-  constexpr int NS = BK / 32;
-  static_assert(NS % 2 == 0, "slice parity must repeat per step");
+  constexpr int NS = BK / 32 / KG;  // slices of each K step per K group
+  static_assert(NS % 2 == 0 && NS * KG * 32 == BK, "slice parity must repeat per step");
+  const int s0 = kg * NS;  // this group's first slice of a step
   v4i af[2][FM], bf[2][FN];
   // A producer's transfers per stage: kPer kIns; the others have none outstanding.
   if (kt_count < STAGES) wait_vmcnt<0>();
   else if (producer) wait_vmcnt<(STAGES - 1) * kPer * kIns>();
   __builtin_amdgcn_s_barrier();
-  read_frags<FM, FN>(af[0], bf[0], smem, a_row_off, b_row_off, (kh ^ rsw) << 4);
+  read_frags<FM, FN>(af[0], bf[0], smem, a_row_off, b_row_off, ((2 * s0 + kh) ^ rsw) << 4);
 
   for (int kt = 0; kt < kt_count; ++kt) {
     const uint8_t *stage = smem + (kt % STAGES) * kStage;
@@ -411,7 +512,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int bid, uint8_t *s
       const int cur = s & 1;
       if (s + 1 < NS) {
         read_frags<FM, FN>(af[cur ^ 1], bf[cur ^ 1], stage, a_row_off, b_row_off,
-                           ((2 * (s + 1) + kh) ^ rsw) << 4);
+                           ((2 * (s0 + s + 1) + kh) ^ rsw) << 4);
       } else {
         // lgkmcnt(0), through the builtin so that the compiler's own wait insertion
         // sees it on every path into the last slice (else it waits there for the next
@@ -426,7 +527,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int bid, uint8_t *s
         __builtin_amdgcn_s_barrier();
         if (kt + STAGES < kt_count) issue(kt + STAGES);
         read_frags<FM, FN>(af[cur ^ 1], bf[cur ^ 1], smem + ((kt + 1) % STAGES) * kStage,
-                           a_row_off, b_row_off, (kh ^ rsw) << 4);
+                           a_row_off, b_row_off, ((2 * s0 + kh) ^ rsw) << 4);
       }
       if (s + 1 < NS) {
         // The next slice's fragment reads go one between each of the first MFMAs, so
@@ -461,62 +562,97 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int bid, uint8_t *s
   // Every wave has finished reading the stages: reuse the LDS for the epilogue.
   constexpr int kRegion =
       32 * ((EPI == kEpiSwiglu ? 16 * FN : 32 * FN) * (EPI == kEpiAcc ? 4 : 2) + 16);
-  if constexpr (kRegion * kWaves <= STAGES * kStage) {
+  if constexpr (KG > 1) {
+    // Groups 1.. leave their sums in LDS after group 0's epilogue regions; group 0
+    // adds them. 16-byte pieces, lane-consecutive: no bank conflicts.
+    constexpr int kSum = kCw * FM * FN * 64 * 64;  // bytes of one group's sums
+    static_assert(kRegion * kCw + (KG - 1) * kSum <= STAGES * kStage, "K-group LDS");
     __syncthreads();
-    store_tile_lds<EPI, FM, FN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, fr, kh, lane,
-                                smem + wave * kRegion);
+    if (kg > 0) {
+      uint8_t *sums = smem + kRegion * kCw + (kg - 1) * kSum + cw * FM * FN * 64 * 64;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<v4i *>(sums + (((i * FN + j) * 4 + q) * 64 + lane) * 16) =
+                v4i{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+    }
+    __syncthreads();
+    if (kg > 0) return;
+#pragma unroll
+    for (int k = 1; k < KG; ++k) {
+      const uint8_t *sums = smem + kRegion * kCw + (k - 1) * kSum + cw * FM * FN * 64 * 64;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const v4i v = *reinterpret_cast<const v4i *>(sums + (((i * FN + j) * 4 + q) * 64 + lane) * 16);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] += v[e];
+          }
+    }
+    store_tile_lds<EPI, FM, FN, BM, BN>(g, split, acc, m0, n0, wm * WTM, wn * WTN, fr, kh, lane,
+                                        smem + cw * kRegion, smem + STAGES * kStage);
+  } else if constexpr (kRegion * kWaves <= STAGES * kStage) {
+    __syncthreads();
+    store_tile_lds<EPI, FM, FN, BM, BN>(g, split, acc, m0, n0, wm * WTM, wn * WTN, fr, kh, lane,
+                                        smem + wave * kRegion, smem + STAGES * kStage);
   } else {  // int32 output of the 256x256 tile: 135 KiB would not fit; direct stores
-    store_tile<EPI, FM, FN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, fr, kh);
+    store_tile<EPI, FM, FN>(g, split, acc, m0 + wm * WTM, n0 + wn * WTN, fr, kh);
   }
 }
 
-template <int BM, int BN, int WM, int WN, int BK, int STAGES, int EPI>
-__global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
+template <int BM, int BN, int WM, int WN, int BK, int STAGES, int EPI, int KG = 1>
+__global__ __launch_bounds__(WM *WN *KG * 64) void gemm_kernel(GemmArgs g) {
   extern __shared__ __align__(16) uint8_t smem[];
-  gemm_tile<BM, BN, WM, WN, BK, STAGES, EPI>(g, blockIdx.x, smem);
+  gemm_tile<BM, BN, WM, WN, BK, STAGES, EPI, KG>(g, blockIdx.x, smem);
 }
 
-template <int BM, int BN, int WM, int WN, int BK, int STAGES>
+template <int BM, int BN, int WM, int WN, int BK, int STAGES, int KG = 1>
 struct TileConfig {
-  static constexpr int kThreads = WM * WN * 64;
-  static constexpr size_t kLds = (size_t)STAGES * (BM + BN) * BK;
+  static constexpr int kThreads = WM * WN * KG * 64;
+  static constexpr size_t kLds = (size_t)STAGES * (BM + BN) * BK + EpiOperands<BM, BN>::kBytes;
 };
 
-template <int BM, int BN, int WM, int WN, int BK, int STAGES>
+template <int BM, int BN, int WM, int WN, int BK, int STAGES, int KG = 1>
 hipError_t launch_tile(int epi, hipStream_t stream, const GemmArgs &a) {
-  using T = TileConfig<BM, BN, WM, WN, BK, STAGES>;
+  using T = TileConfig<BM, BN, WM, WN, BK, STAGES, KG>;
   const int tiles = ((a.m + BM - 1) / BM) * (a.n / BN);
   const int k_steps = a.k / BK;
   const int splits = a.k_split_steps > 0 ? (k_steps + a.k_split_steps - 1) / a.k_split_steps : 1;
   dim3 grid(tiles, splits), block(T::kThreads);
   switch (epi) {
     case kEpiPlain:
-      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiPlain>), grid, block, T::kLds, stream, a);
+      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiPlain, KG>), grid, block, T::kLds, stream, a);
       break;
     case kEpiResid:
-      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiResid>), grid, block, T::kLds, stream, a);
+      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiResid, KG>), grid, block, T::kLds, stream, a);
       break;
     case kEpiSwiglu:
-      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiSwiglu>), grid, block, T::kLds, stream, a);
+      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiSwiglu, KG>), grid, block, T::kLds, stream, a);
       break;
     case kEpiBias:
-      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiBias>), grid, block, T::kLds, stream, a);
+      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiBias, KG>), grid, block, T::kLds, stream, a);
       break;
     default:
-      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiAcc>), grid, block, T::kLds, stream, a);
+      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiAcc, KG>), grid, block, T::kLds, stream, a);
       break;
   }
   return hipGetLastError();
 }
 
-template <int BM, int BN, int WM, int WN, int BK, int STAGES>
+template <int BM, int BN, int WM, int WN, int BK, int STAGES, int KG = 1>
 hipError_t set_lds_tile() {
-  using T = TileConfig<BM, BN, WM, WN, BK, STAGES>;
-  const void *fns[5] = {reinterpret_cast<const void *>(gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiPlain>),
-                        reinterpret_cast<const void *>(gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiResid>),
-                        reinterpret_cast<const void *>(gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiSwiglu>),
-                        reinterpret_cast<const void *>(gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiBias>),
-                        reinterpret_cast<const void *>(gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiAcc>)};
+  using T = TileConfig<BM, BN, WM, WN, BK, STAGES, KG>;
+  const void *fns[5] = {reinterpret_cast<const void *>(gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiPlain, KG>),
+                        reinterpret_cast<const void *>(gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiResid, KG>),
+                        reinterpret_cast<const void *>(gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiSwiglu, KG>),
+                        reinterpret_cast<const void *>(gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiBias, KG>),
+                        reinterpret_cast<const void *>(gemm_kernel<BM, BN, WM, WN, BK, STAGES, kEpiAcc, KG>)};
   for (const void *f : fns) {
     hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)T::kLds);
     if (e != hipSuccess) return e;
@@ -584,6 +720,26 @@ constexpr int kMidWm = K2W8_MID_WM, kMidWn = 8 / kMidWm;
 #define K2W8_S128_STAGES 2
 #endif
 constexpr int kS64Stages = K2W8_S64_STAGES, kS128Stages = K2W8_S128_STAGES;
+// Split-K slices: 128x128 tiles of eight waves (2 x 4, each 64x32), whose lower four
+// waves issue the transfers, with three stages (one workgroup per CU, two K steps in
+// flight). Against four waves and two stages: M=256 down projection 19.8 -> 18.1 us,
+// M=512 26.4 -> 25.0 us. Deeper 64x64 pipelines (six or eight stages, one workgroup
+// per CU) were slower (QKV at M=256: 8.6 -> 9.1-9.4 us).
+#ifndef K2W8_SPLIT_WN
+#define K2W8_SPLIT_WN 4
+#endif
+#ifndef K2W8_SPLIT_STAGES
+#define K2W8_SPLIT_STAGES 3
+#endif
+constexpr int kSplitStages = K2W8_SPLIT_STAGES, kSplitWn = K2W8_SPLIT_WN;
+#ifndef K2W8_S64_KG
+#define K2W8_S64_KG 2
+#endif
+constexpr int kS64Kg = K2W8_S64_KG;
+#ifndef K2W8_T12864_STAGES
+#define K2W8_T12864_STAGES 3
+#endif
+constexpr int k12864Stages = K2W8_T12864_STAGES;
 
 int device_cus() {
   static int cached[64];
@@ -616,8 +772,10 @@ hipError_t configure_gemm_lds() {
   if (e == hipSuccess) e = gemm::set_lds_tile<256, 192, 4, 2, 128, 2>();
   if (e == hipSuccess) e = gemm::set_lds_tile<256, 128, kMidWm, kMidWn, 128, 2>();
   if (e == hipSuccess) e = gemm::set_lds_tile<128, 128, 2, 2, 128, kS128Stages>();
-  if (e == hipSuccess) e = gemm::set_lds_tile<64, 64, 2, 2, 128, kS64Stages>();
+  if (e == hipSuccess) e = gemm::set_lds_tile<64, 64, 2, 2, 128, kS64Stages, kS64Kg>();
+  if (e == hipSuccess) e = gemm::set_lds_tile<128, 64, 4, 2, 128, k12864Stages>();
   if (e == hipSuccess) e = gemm::set_lds_tile<256, 128, kMidWm, kMidWn, 128, 3>();
+  if (e == hipSuccess) e = gemm::set_lds_tile<128, 128, 2, kSplitWn, 128, kSplitStages>();
   if (e == hipSuccess) e = configure_skinny_lds();
   return e;
 }
@@ -631,9 +789,12 @@ int splitk_steps(const GemmLaunch &l, int64_t cus, size_t workspace_bytes) {
   const int64_t tiles = ((l.m + 127) / 128) * (l.n / 128);
   const int64_t k_steps = l.k / 128;
   if (tiles * 2 > cus || k_steps < 2 * K2W8_SPLITK_MIN_STEPS) return 0;
-  int64_t splits = (cus + tiles - 1) / tiles;
+  // As many splits as keep the grid to one workgroup per CU (one round): a second,
+  // partial round costs more than the K steps it takes off each slice.
+  int64_t splits = cus / tiles;
   if (splits > k_steps / K2W8_SPLITK_MIN_STEPS) splits = k_steps / K2W8_SPLITK_MIN_STEPS;
   const int64_t slice_bytes = l.m * l.n * 4;
+  if (slice_bytes >= (int64_t)1 << 31) return 0;  // buffer offsets within a slice are 32-bit
   const int64_t fit = (int64_t)workspace_bytes / slice_bytes;
   if (splits > fit) splits = fit;
   if (splits < 2) return 0;
@@ -701,8 +862,12 @@ hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &l) {
   if (tiles(128, 128) >= kCus) return gemm::launch_tile<128, 128, 2, 2, 128, kS128Stages>(epilogue, stream, a);
   // 64x64 tiles read every operand byte 4x as often as 128x128 ones: past K=4096 the
   // split-K pass over 128x128 tiles moves fewer bytes.
+#ifndef K2W8_NO_12864
+  if (tiles(128, 64) >= kCus && l.k <= 4096)
+    return gemm::launch_tile<128, 64, 4, 2, 128, k12864Stages>(epilogue, stream, a);
+#endif
   if (tiles(64, 64) >= kCus && l.k <= 4096)
-    return gemm::launch_tile<64, 64, 2, 2, 128, kS64Stages>(epilogue, stream, a);
+    return gemm::launch_tile<64, 64, 2, 2, 128, kS64Stages, kS64Kg>(epilogue, stream, a);
   const Workspace ws = l.workspace ? *l.workspace : splitk_workspace(stream);
   // A caller that passes a fixed workspace and requires it: a shape that would split K
   // but whose two slices do not fit is refused before anything is launched.
@@ -719,12 +884,12 @@ hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &l) {
       p.ldc = (int)l.n;
       p.k_split_steps = per;
       p.split_stride = l.m * l.n;
-      hipError_t e = gemm::launch_tile<128, 128, 2, 2, 128, kS128Stages>(kEpiAcc, stream, p);
+      hipError_t e = gemm::launch_tile<128, 128, 2, kSplitWn, 128, kSplitStages>(kEpiAcc, stream, p);
       if (e != hipSuccess) return e;
       return launch_splitk_reduce(epilogue, stream, parts, splits, l.m * l.n, a);
     }
   }
-  return gemm::launch_tile<64, 64, 2, 2, 128, kS64Stages>(epilogue, stream, a);
+  return gemm::launch_tile<64, 64, 2, 2, 128, kS64Stages, kS64Kg>(epilogue, stream, a);
 }
 #endif
 

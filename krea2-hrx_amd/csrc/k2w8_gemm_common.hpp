@@ -60,6 +60,11 @@ __device__ __forceinline__ void dma16(uint32_t lds, const int8_t *base, uint32_t
   asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(uniform_ptr(base)), "{m0}"(lds) : "memory");
 }
 
+// The 4-byte form: lane l writes LDS bytes [lds + 4 l, lds + 4 l + 4).
+__device__ __forceinline__ void dma4(uint32_t lds, const void *base, uint32_t voff) {
+  asm volatile("global_load_lds_dword %0, %1" ::"v"(voff), "s"(uniform_ptr(base)), "{m0}"(lds) : "memory");
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
@@ -77,6 +82,22 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int m
   const int rows_in_group = min(tiles_m - first_m, m_group);
   tm = first_m + in_group % rows_in_group;
   tn = in_group / rows_in_group;
+}
+
+// Output tile and K split of workgroup (x, y) of a split-K grid (tiles x splits).
+// Workgroups go to the XCDs in turn (linear id mod kXcds); XCD j takes one contiguous
+// run of the work order, which is m-tile fastest, then n-tile, then split. The m-tiles
+// of one weight slice then share an XCD's L2, and each XCD reads the A columns of one
+// or two K splits only (M=256 down projection: 50 -> 32 MB read past the L2s).
+__device__ __forceinline__ void split_tile_of(int x, int y, int tiles, int splits, int tiles_m, int &tm,
+                                              int &tn, int &split) {
+  const int total = tiles * splits, linear = y * tiles + x;
+  const int xcd = linear % kXcds, base = total / kXcds, rem = total - base * kXcds;
+  const int w = xcd * base + min(xcd, rem) + linear / kXcds;
+  tm = w % tiles_m;
+  const int rest = w / tiles_m, tiles_n = tiles / tiles_m;
+  tn = rest % tiles_n;
+  split = rest / tiles_n;
 }
 
 // This wave's A and B fragments of one 32-byte K slice: LDS chunk offset `c` of each

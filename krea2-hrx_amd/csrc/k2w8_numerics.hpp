@@ -96,18 +96,57 @@ __device__ __forceinline__ float sigmoid_exp(float x) {
 // (within 1 ulp) and one residual correction, res = 1 - d*y exactly by fma, then
 // y + res*y rounded once, give the correctly rounded quotient: checked on the device
 // for every such d. Larger d (subnormal quotients, and infinity) take the IEEE
-// division, which a wave only runs when one of its lanes needs it.
-__device__ __forceinline__ float sigmoid(float g) {
-  float e = sigmoid_exp(0.0f - g);
-  float den = 1.0f + e;
+// division. sigmoid_fast is the common path and returns d; sigmoid_fix redoes the
+// quotient where d is that large.
+__device__ __forceinline__ float sigmoid_fast(float g, float &den) {
+  const float e = sigmoid_exp(0.0f - g);
+  den = 1.0f + e;
   float y = __builtin_amdgcn_rcpf(den);
-  float res = __builtin_fmaf(-den, y, 1.0f);
-  y = __builtin_fmaf(res, y, y);
+  const float res = __builtin_fmaf(-den, y, 1.0f);
+  return __builtin_fmaf(res, y, y);
+}
+
+__device__ __forceinline__ float sigmoid_fix(float y, float den) { return den >= 0x1p126f ? 1.0f / den : y; }
+
+// One sigmoid; the division runs only in a wave with a lane that needs it.
+__device__ __forceinline__ float sigmoid(float g) {
+  float den;
+  float y = sigmoid_fast(g, den);
   if (__builtin_expect(den >= 0x1p126f, 0)) {
     asm volatile("");  // keeps the division out of the common path
     y = 1.0f / den;
   }
   return y;
+}
+
+// The SwiGLU products of N gate and up values (N even, each already rounded to bf16):
+// g[k] <- bf16(bf16(g[k] * sigmoid(g[k])) * u[k]), the values of the per-element form.
+// Every sigmoid's common path runs before the one branch to the division path (taken
+// only by a wave with a lane that needs it), so the N operation chains interleave
+// instead of each ending at a branch of its own.
+template <int N>
+__device__ __forceinline__ void swiglu_products(float (&g)[N], const float (&u)[N]) {
+  static_assert(N % 2 == 0, "pairs");
+  float y[N], den[N];
+  bool slow = false;
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    y[k] = sigmoid_fast(g[k], den[k]);
+    slow |= den[k] >= 0x1p126f;
+  }
+  if (__builtin_expect(slow, 0)) {
+#pragma unroll
+    for (int k = 0; k < N; ++k) y[k] = sigmoid_fix(y[k], den[k]);
+  }
+#pragma unroll
+  for (int k = 0; k < N; k += 2) {
+    float s0 = g[k] * y[k], s1 = g[k + 1] * y[k + 1];
+    bf16_round2(s0, s1);
+    float p0 = s0 * u[k], p1 = s1 * u[k + 1];
+    bf16_round2(p0, p1);
+    g[k] = p0;
+    g[k + 1] = p1;
+  }
 }
 
 }  // namespace k2w8

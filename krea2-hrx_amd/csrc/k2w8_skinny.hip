@@ -240,7 +240,7 @@ __global__ __launch_bounds__(WAVES * 64) void stream_kernel(Args g) {
     const float4 us = kPairRows ? gs[0] : ws[RBK - 1];
     const float usv[4] = {us.x, us.y, us.z, us.w};
     const v4i gate = sum[0], up = kPairRows ? pair_up : sum[RBK - 1];
-    uint32_t packed[2];
+    float gv[4], uv[4];
 #pragma unroll
     for (int e = 0; e < 4; e += 2) {
       float g0 = ((float)gate[e] * gsv[e]) * as, g1 = ((float)gate[e + 1] * gsv[e + 1]) * as;
@@ -248,12 +248,10 @@ __global__ __launch_bounds__(WAVES * 64) void stream_kernel(Args g) {
       float u1 = ((float)up[e + 1] * usv[e + 1]) * as;
       bf16_round2(g0, g1);
       bf16_round2(u0, u1);
-      float s0 = g0 * sigmoid(g0), s1 = g1 * sigmoid(g1);
-      bf16_round2(s0, s1);
-      float p0 = s0 * u0, p1 = s1 * u1;
-      bf16_round2(p0, p1);
-      packed[e >> 1] = f16_pack2(p0, p1);
+      gv[e] = g0; gv[e + 1] = g1; uv[e] = u0; uv[e + 1] = u1;
     }
+    swiglu_products(gv, uv);
+    const uint32_t packed[2] = {f16_pack2(gv[0], gv[1]), f16_pack2(gv[2], gv[3])};
     const int col = kPairRows ? 16 * (blockIdx.x >> 1) + 8 * (blockIdx.x & 1) : n0 >> 1;
     uint16_t *out = static_cast<uint16_t *>(g.c) + (int64_t)tok * (g.n >> 1) + col + 4 * kq;
     *reinterpret_cast<uint2 *>(out) = make_uint2(packed[0], packed[1]);
