@@ -64,7 +64,8 @@ __global__ __launch_bounds__(512) void prepare_gemm_kernel(PrepareArgs p, gemm::
 template <int kKind, int T, int BM, int BN>
 hipError_t launch(hipStream_t stream, const PrepareArgs &p, const gemm::GemmArgs &g, int cus) {
   const void *fn = reinterpret_cast<const void *>(prepare_gemm_kernel<kKind, T, BM, BN>);
-  const size_t stage_lds = (size_t)2 * (BM + BN) * 128 + gemm::EpiOperands<BM, BN>::kBytes;
+  const size_t stage_lds = (size_t)2 * (BM + BN) * 128 + gemm::EpiOperands<BM, BN>::kBytes +
+                           gemm::EpiStaging<BM, BN, 4, 2, 128, 2, 1>::kOverflow;
   const size_t factor_lds = kKind == kNorm ? (size_t)(p.width / 16) * kFactorStride * 16 : 0;
   const size_t lds = stage_lds > factor_lds ? stage_lds : factor_lds;
   static hipError_t configured = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);

@@ -174,6 +174,21 @@ struct EpiOperands {
   static constexpr int kBytes = BN * 8 + BM * 4;
 };
 
+// The epilogue's per-wave LDS regions (32 rows of the wave's output columns plus 16
+// bytes per row; 16-bit outputs). When a wave leaves the K loop, every stage but the
+// last one read is free (the last barrier of the loop came after the reads of the
+// others, and no transfer targets them any more), so the regions go in such a stage,
+// and those that do not fit in it in an overflow area after the epilogue operands:
+// each wave then starts its epilogue without waiting for the others at a barrier
+// (the two waves of a SIMD leave the loop about a thousand cycles apart).
+template <int BM, int BN, int WM, int WN, int BK, int STAGES, int KG>
+struct EpiStaging {
+  static constexpr int kWaves = WM * WN, kFN = BN / WN / 32, kStage = (BM + BN) * BK;
+  static constexpr int kRegion = 32 * (32 * kFN * 2 + 16);
+  static constexpr int kPerStage = kStage / kRegion < kWaves ? kStage / kRegion : kWaves;
+  static constexpr int kOverflow = KG == 1 ? (kWaves - kPerStage) * kRegion : 0;
+};
+
 template <int EPI, int BM, int BN>
 __device__ __forceinline__ void stage_epi_operands(const GemmArgs &g, int m0, int n0, int lane,
                                                    uint32_t lds) {
@@ -220,6 +235,30 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs &g, int split, v16
   const int out_base = EPI == kEpiSwiglu ? n_base / 2 : n_base;
   const float *ws_lds = reinterpret_cast<const float *>(ops + E::kWs) + n_off;
   const float *as_lds = reinterpret_cast<const float *>(ops + E::kAs) + m_off;
+  // Per-channel vectors of this lane's channels: n = n_base + 32j + 8q + 4kh + r
+  // (SwiGLU: registers 8-15 are the up channels, 16 further on). Read once for all row
+  // blocks where the registers allow (the 256x256 tiles' SwiGLU and bias epilogues
+  // would spill: they read them per block).
+  constexpr bool kHoist = EPI != kEpiAcc && (FN <= 2 || EPI == kEpiPlain || EPI == kEpiResid);
+  auto channel_vectors = [&](int j, float *ws, float *extra) {
+    const int nb = j * 32 + kh * 4;  // within the wave's columns
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int ch = (EPI == kEpiSwiglu && q >= 2) ? nb + 16 + 8 * (q - 2) : nb + 8 * q;
+      const float4 v = *reinterpret_cast<const float4 *>(ws_lds + ch);
+      ws[4 * q] = v.x; ws[4 * q + 1] = v.y; ws[4 * q + 2] = v.z; ws[4 * q + 3] = v.w;
+      if (EPI == kEpiBias) {
+        const uint2 b = *reinterpret_cast<const uint2 *>(ops + E::kExtra + 2 * (n_off + ch));
+        extra[4 * q] = f16_value(b.x & 0xffffu); extra[4 * q + 1] = f16_value(b.x >> 16);
+        extra[4 * q + 2] = f16_value(b.y & 0xffffu); extra[4 * q + 3] = f16_value(b.y >> 16);
+      }
+    }
+  };
+  float wsv[kHoist ? FN : 1][16], exv[kHoist && EPI == kEpiBias ? FN : 1][16];
+  if constexpr (kHoist) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) channel_vectors(j, wsv[j], exv[EPI == kEpiBias ? j : 0]);
+  }
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const float as = EPI == kEpiAcc ? 1.0f : as_lds[i * 32 + fr];
@@ -234,21 +273,10 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs &g, int split, v16
               v4i{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
         continue;
       }
-      // Per-channel vectors of this lane's channels: n = n_base + 32j + 8q + 4kh + r
-      // (SwiGLU: registers 8-15 are the up channels, 16 further on).
-      float ws[16], extra[16];
-      const int nb = j * 32 + kh * 4;  // within the wave's columns
-#pragma unroll
-      for (int q = 0; q < 4 && EPI != kEpiAcc; ++q) {
-        const int ch = (EPI == kEpiSwiglu && q >= 2) ? nb + 16 + 8 * (q - 2) : nb + 8 * q;
-        const float4 v = *reinterpret_cast<const float4 *>(ws_lds + ch);
-        ws[4 * q] = v.x; ws[4 * q + 1] = v.y; ws[4 * q + 2] = v.z; ws[4 * q + 3] = v.w;
-        if (EPI == kEpiBias) {
-          const uint2 b = *reinterpret_cast<const uint2 *>(ops + E::kExtra + 2 * (n_off + ch));
-          extra[4 * q] = f16_value(b.x & 0xffffu); extra[4 * q + 1] = f16_value(b.x >> 16);
-          extra[4 * q + 2] = f16_value(b.y & 0xffffu); extra[4 * q + 3] = f16_value(b.y >> 16);
-        }
-      }
+      float ws_b[kHoist ? 1 : 16], extra_b[kHoist ? 1 : 16];
+      if constexpr (!kHoist) channel_vectors(j, ws_b, extra_b);
+      const float *ws = kHoist ? wsv[j] : ws_b;
+      const float *extra = kHoist ? exv[EPI == kEpiBias ? j : 0] : extra_b;
       if (EPI == kEpiSwiglu) {
         // registers 0-7: gate channels 8q+4kh+r (q<2), 8-15: the matching ups; the
         // products of the block's FN x 8 pairs are formed together (swiglu_products)
@@ -559,7 +587,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int bid, uint8_t *s
     }
   }
 
-  // Every wave has finished reading the stages: reuse the LDS for the epilogue.
+  // The epilogue's LDS staging region of this wave (see EpiStaging).
   constexpr int kRegion =
       32 * ((EPI == kEpiSwiglu ? 16 * FN : 32 * FN) * (EPI == kEpiAcc ? 4 : 2) + 16);
   if constexpr (KG > 1) {
@@ -597,6 +625,14 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int bid, uint8_t *s
     }
     store_tile_lds<EPI, FM, FN, BM, BN>(g, split, acc, m0, n0, wm * WTM, wn * WTN, fr, kh, lane,
                                         smem + cw * kRegion, smem + STAGES * kStage);
+  } else if constexpr ((kWaves - (kStage / kRegion < kWaves ? kStage / kRegion : kWaves)) * kRegion <=
+                       EpiStaging<BM, BN, WM, WN, BK, STAGES, KG>::kOverflow) {
+    constexpr int kPer = kStage / kRegion < kWaves ? kStage / kRegion : kWaves;
+    const int free_stage = kt_count >= 2 ? (kt_count - 2) % STAGES : 1;
+    uint8_t *region = wave < kPer ? smem + free_stage * kStage + wave * kRegion
+                                  : smem + STAGES * kStage + EpiOperands<BM, BN>::kBytes + (wave - kPer) * kRegion;
+    store_tile_lds<EPI, FM, FN, BM, BN>(g, split, acc, m0, n0, wm * WTM, wn * WTN, fr, kh, lane, region,
+                                        smem + STAGES * kStage);
   } else if constexpr (kRegion * kWaves <= STAGES * kStage) {
     __syncthreads();
     store_tile_lds<EPI, FM, FN, BM, BN>(g, split, acc, m0, n0, wm * WTM, wn * WTN, fr, kh, lane,
@@ -615,7 +651,8 @@ __global__ __launch_bounds__(WM *WN *KG * 64) void gemm_kernel(GemmArgs g) {
 template <int BM, int BN, int WM, int WN, int BK, int STAGES, int KG = 1>
 struct TileConfig {
   static constexpr int kThreads = WM * WN * KG * 64;
-  static constexpr size_t kLds = (size_t)STAGES * (BM + BN) * BK + EpiOperands<BM, BN>::kBytes;
+  static constexpr size_t kLds = (size_t)STAGES * (BM + BN) * BK + EpiOperands<BM, BN>::kBytes +
+                                 EpiStaging<BM, BN, WM, WN, BK, STAGES, KG>::kOverflow;
 };
 
 template <int BM, int BN, int WM, int WN, int BK, int STAGES, int KG = 1>
