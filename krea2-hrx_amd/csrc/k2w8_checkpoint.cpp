@@ -18,6 +18,7 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <set>
 #include <memory>
 #include <string>
 #include <vector>
@@ -317,11 +318,25 @@ struct k2w8_checkpoint {
   bool has(const std::string &name) const { return entries.count(name) != 0; }
   const uint8_t *bytes(const Entry &e) const { return data + e.begin; }
 
-  // file.rs:124-129
+  // Blocks are numbered from 0 without gaps; a block exists when its first attention
+  // projection does (the rule of file.rs:124-129): the count is the first number
+  // missing from the checkpoint's `blocks.<n>.attn.wq.weight` names.
   int64_t block_count() const {
-    int64_t i = 0;
-    while (i < (int64_t)entries.size() && has(format("blocks.%lld.attn.wq.weight", (long long)i))) ++i;
-    return i;
+    static const std::string head = "blocks.", tail = ".attn.wq.weight";
+    std::set<int64_t> present;
+    for (const auto &kv : entries) {
+      const std::string &n = kv.first;
+      if (n.size() <= head.size() + tail.size() || n.compare(0, head.size(), head) != 0 ||
+          n.compare(n.size() - tail.size(), tail.size(), tail) != 0)
+        continue;
+      const std::string digits = n.substr(head.size(), n.size() - head.size() - tail.size());
+      if (digits.empty() || digits.size() > 9 || digits.find_first_not_of("0123456789") != std::string::npos)
+        continue;
+      present.insert(std::stoll(digits));
+    }
+    int64_t count = 0;
+    while (present.count(count)) ++count;
+    return count;
   }
 };
 
@@ -340,92 +355,91 @@ struct Span {
   int64_t file_bytes() const { return host.empty() ? rows * row_bytes : (int64_t)host.size(); }
 };
 
-// plan.rs:61-74
-const Entry &int8_rows(const k2w8_checkpoint &file, const std::string &name) {
-  const Entry &t = file.get(name + ".weight");
-  if (t.dtype != K2W8_DTYPE_I8 || t.shape.size() != 2)
-    throw Error{format("%s.weight is not int8 ConvRot rows (%s)", name.c_str(), file.path.c_str())};
-  if (t.shape[0] == 0 || t.shape[1] == 0)
-    throw Error{format("invalid weight shape or size in %s", name.c_str())};
-  return t;
+// A GEMM operand's rows on the device (the layout of plan.rs:61-85, 154-230): int8
+// weight rows of K bytes, each padded to the GEMM pitch, with one f32 scale per row in a
+// span of their own. The device rows are a sequence of runs of source rows; the scales
+// follow the same runs.
+struct RowRun {
+  int part;               // index into the operand's parts
+  int64_t first, count;   // source rows [first, first + count)
+};
+
+// The device row order of `parts` (their row counts in `rows`): the parts one after
+// another (group 0), or taken in turns, `group` rows of each part per turn. The turns
+// need every part to have the same number of rows, a whole number of groups.
+std::vector<RowRun> row_order(const std::string &operand, const std::vector<int64_t> &rows, int64_t group) {
+  std::vector<RowRun> runs;
+  if (group == 0) {
+    for (size_t p = 0; p < rows.size(); ++p) runs.push_back(RowRun{(int)p, 0, rows[p]});
+    return runs;
+  }
+  for (int64_t r : rows)
+    if (r != rows[0] || r % group != 0)
+      throw Error{format("%s takes its parts %lld rows at a time in turn: they need equal row counts "
+                         "that are whole multiples of it", operand.c_str(), (long long)group)};
+  for (int64_t first = 0; first < rows[0]; first += group)
+    for (size_t p = 0; p < rows.size(); ++p) runs.push_back(RowRun{(int)p, first, group});
+  return runs;
 }
 
-// plan.rs:76-85
-const Entry &scales(const k2w8_checkpoint &file, const std::string &name, int64_t rows) {
-  const Entry &t = file.get(name + ".weight_scale");
-  if (t.dtype != K2W8_DTYPE_F32) throw Error{format("%s.weight_scale is not float32", name.c_str())};
-  if ((int64_t)(t.end - t.begin) != rows * 4) throw Error{format("scale count in %s", name.c_str())};
-  return t;
-}
-
-// plan.rs:154-230: one GEMM operand and its scales; group 0 concatenates the parts'
-// rows, group g interleaves them g rows at a time.
+// One operand: its weight span (rows gathered straight from the file) and its scale
+// span (assembled on the host in the same row order).
 void operand(const k2w8_checkpoint &file, const std::string &out, const std::vector<std::string> &parts,
              int64_t group, Span &weights, Span &scale_span) {
-  std::vector<const Entry *> tensors;
-  for (const auto &part : parts) tensors.push_back(&int8_rows(file, part));
-  const int64_t row_bytes = tensors[0]->shape[1];
-  int64_t rows = 0;
-  for (const Entry *t : tensors) {
-    if (t->shape[1] != row_bytes) throw Error{format("mismatched K in %s", out.c_str())};
-    rows += t->shape[0];
+  std::vector<const Entry *> w(parts.size()), sc(parts.size());
+  std::vector<int64_t> rows(parts.size());
+  for (size_t p = 0; p < parts.size(); ++p) {
+    w[p] = &file.get(parts[p] + ".weight");
+    if (w[p]->dtype != K2W8_DTYPE_I8 || w[p]->shape.size() != 2 || w[p]->shape[0] == 0 || w[p]->shape[1] == 0)
+      throw Error{format("%s.weight in %s must be a non-empty int8 matrix of ConvRot rows", parts[p].c_str(),
+                         file.path.c_str())};
+    rows[p] = w[p]->shape[0];
+    if (w[p]->shape[1] != w[0]->shape[1])
+      throw Error{format("%s: %s has rows of %lld bytes and %s of %lld; one operand has one K", out.c_str(),
+                         parts[0].c_str(), (long long)w[0]->shape[1], parts[p].c_str(), (long long)w[p]->shape[1])};
+    sc[p] = &file.get(parts[p] + ".weight_scale");
+    if (sc[p]->dtype != K2W8_DTYPE_F32 || (int64_t)(sc[p]->end - sc[p]->begin) != rows[p] * 4)
+      throw Error{format("%s.weight_scale must hold one float32 per weight row (%lld)", parts[p].c_str(),
+                         (long long)rows[p])};
   }
-  const int64_t pitch = k2w8_shape_gemm_pitch(row_bytes);
+  const std::vector<RowRun> runs = row_order(out, rows, group);
+  const int64_t k = w[0]->shape[1];
   weights = Span{};
-  weights.rows = rows;
-  weights.row_bytes = row_bytes;
-  weights.device_row_bytes = pitch;
-  weights.device_bytes = rows * pitch;
-  std::vector<uint8_t> scale_bytes((size_t)rows * 4);
-  int64_t written = 0;
-  if (group == 0) {
-    for (size_t i = 0; i < parts.size(); ++i) {
-      const int64_t count = tensors[i]->shape[0];
-      weights.segments.push_back(Segment{parts[i] + ".weight", 0, count});
-      const Entry &src = scales(file, parts[i], count);
-      memcpy(scale_bytes.data() + written * 4, file.bytes(src), (size_t)count * 4);
-      written += count;
-    }
-  } else {
-    if (tensors.size() != 2 || tensors[0]->shape[0] != tensors[1]->shape[0] ||
-        tensors[0]->shape[0] % group != 0)
-      throw Error{format("interleave shape in %s", out.c_str())};
-    const int64_t half = tensors[0]->shape[0];
-    const Entry *src[2] = {&scales(file, parts[0], half), &scales(file, parts[1], half)};
-    for (int64_t start = 0; start < half; start += group) {
-      for (int p = 0; p < 2; ++p) {
-        weights.segments.push_back(Segment{parts[p] + ".weight", start, start + group});
-        memcpy(scale_bytes.data() + written * 4, file.bytes(*src[p]) + start * 4, (size_t)group * 4);
-        written += group;
-      }
-    }
+  weights.row_bytes = k;
+  weights.device_row_bytes = k2w8_shape_gemm_pitch(k);
+  std::vector<uint8_t> scale_bytes;
+  for (const RowRun &run : runs) {
+    weights.segments.push_back(Segment{parts[run.part] + ".weight", run.first, run.first + run.count});
+    weights.rows += run.count;
+    const uint8_t *src = file.bytes(*sc[run.part]) + run.first * 4;
+    scale_bytes.insert(scale_bytes.end(), src, src + run.count * 4);
   }
+  weights.device_bytes = weights.rows * weights.device_row_bytes;
   scale_span = Span{};
   scale_span.device_bytes = (int64_t)scale_bytes.size();
   scale_span.host = std::move(scale_bytes);
 }
 
-// plan.rs:233-264: an f32 vector as it is, or upcast exactly from bf16.
+// A norm vector (plan.rs:233-264): float32 as stored, or bfloat16 widened exactly (the
+// bf16 bits become the high half of the f32).
 Span vector(const k2w8_checkpoint &file, const std::string &name) {
   const Entry &t = file.get(name);
-  Span s;
   const int64_t nbytes = (int64_t)(t.end - t.begin);
-  if (t.dtype == K2W8_DTYPE_BF16) {
-    s.host.resize((size_t)nbytes * 2);
-    const uint8_t *src = file.bytes(t);
-    for (int64_t i = 0; i < nbytes / 2; ++i) {
-      const uint32_t bits = (uint32_t)(src[2 * i] | (src[2 * i + 1] << 8)) << 16;
-      memcpy(s.host.data() + 4 * i, &bits, 4);
-    }
-    s.device_bytes = (int64_t)s.host.size();
+  Span s;
+  if (t.dtype == K2W8_DTYPE_F32) {
+    s.rows = 1;
+    s.row_bytes = s.device_row_bytes = s.device_bytes = nbytes;
+    s.segments.push_back(Segment{name, 0, 1});
     return s;
   }
-  if (t.dtype != K2W8_DTYPE_F32) throw Error{format("%s is not float32", name.c_str())};
-  s.device_bytes = nbytes;
-  s.rows = 1;
-  s.row_bytes = nbytes;
-  s.device_row_bytes = nbytes;
-  s.segments.push_back(Segment{name, 0, 1});
+  if (t.dtype != K2W8_DTYPE_BF16) throw Error{format("%s must be float32 or bfloat16", name.c_str())};
+  const uint8_t *src = file.bytes(t);
+  s.host.resize((size_t)nbytes * 2);
+  for (int64_t i = 0; i < nbytes / 2; ++i) {
+    const uint32_t widened = ((uint32_t)src[2 * i] | (uint32_t)src[2 * i + 1] << 8) << 16;
+    memcpy(s.host.data() + 4 * i, &widened, 4);
+  }
+  s.device_bytes = (int64_t)s.host.size();
   return s;
 }
 
@@ -440,42 +454,51 @@ struct k2w8_plan {
 
 namespace {
 
-// plan.rs:88-143
+// What each block uploads (the spans of plan.rs:88-143): four GEMM operands, named by
+// suffix, from their source tensors (the gate|up pair in turns of 16 rows, the layout
+// gemm_i8_swiglu reads), and four norm vectors.
+struct OperandSource {
+  const char *span;
+  std::vector<const char *> parts;
+  int64_t group;
+};
+const OperandSource kOperands[] = {
+    {"qkvg", {"attn.wq", "attn.wk", "attn.wv", "attn.gate"}, 0},
+    {"wo", {"attn.wo"}, 0},
+    {"gu", {"mlp.gate", "mlp.up"}, 16},
+    {"down", {"mlp.down"}, 0},
+};
+const std::pair<const char *, const char *> kVectors[] = {
+    {"prenorm", "prenorm.scale"},
+    {"postnorm", "postnorm.scale"},
+    {"qnorm", "attn.qknorm.qnorm.scale"},
+    {"knorm", "attn.qknorm.knorm.scale"},
+};
+
 std::unique_ptr<k2w8_plan> plan_for(const k2w8_checkpoint &file) {
   auto plan = std::make_unique<k2w8_plan>();
-  const int64_t layers = file.block_count();
-  if (layers == 0) throw Error{format("no transformer blocks in %s", file.path.c_str())};
-  for (int64_t block = 0; block < layers; ++block) {
-    const std::string p = format("blocks.%lld", (long long)block);
-    Span q, s;
-    operand(file, p + ".qkvg", {p + ".attn.wq", p + ".attn.wk", p + ".attn.wv", p + ".attn.gate"}, 0, q, s);
-    plan->spans[p + ".qkvg.q"] = std::move(q);
-    plan->spans[p + ".qkvg.s"] = std::move(s);
-    const std::pair<const char *, std::string> single[2] = {{"wo", p + ".attn.wo"}, {"down", p + ".mlp.down"}};
-    for (const auto &os : single) {
-      operand(file, p + "." + os.first, {os.second}, 0, q, s);
-      plan->spans[p + "." + os.first + ".q"] = std::move(q);
-      plan->spans[p + "." + os.first + ".s"] = std::move(s);
+  plan->layers = file.block_count();
+  if (plan->layers == 0)
+    throw Error{format("no transformer blocks in %s (no blocks.0.attn.wq.weight)", file.path.c_str())};
+  for (int64_t b = 0; b < plan->layers; ++b) {
+    const std::string block = format("blocks.%lld.", (long long)b);
+    for (const OperandSource &op : kOperands) {
+      std::vector<std::string> parts;
+      for (const char *part : op.parts) parts.push_back(block + part);
+      Span weights, scales;
+      operand(file, block + op.span, parts, op.group, weights, scales);
+      plan->spans[block + op.span + ".q"] = std::move(weights);
+      plan->spans[block + op.span + ".s"] = std::move(scales);
     }
-    operand(file, p + ".gu", {p + ".mlp.gate", p + ".mlp.up"}, 16, q, s);
-    plan->spans[p + ".gu.q"] = std::move(q);
-    plan->spans[p + ".gu.s"] = std::move(s);
-    const std::pair<const char *, std::string> vectors[4] = {
-        {"prenorm", p + ".prenorm.scale"},
-        {"postnorm", p + ".postnorm.scale"},
-        {"qnorm", p + ".attn.qknorm.qnorm.scale"},
-        {"knorm", p + ".attn.qknorm.knorm.scale"}};
-    for (const auto &v : vectors) plan->spans[p + "." + v.first] = vector(file, v.second);
+    for (const auto &v : kVectors) plan->spans[block + v.first] = vector(file, block + v.second);
   }
-  // Spans start at 256-byte boundaries in name order.
-  int64_t total = 0;
+  // Device placement: the spans in name order (the map's order), each at the next
+  // 256-byte boundary.
   for (auto &kv : plan->spans) {
-    kv.second.device_offset = total;
-    total += (kv.second.device_bytes + 255) / 256 * 256;
+    kv.second.device_offset = plan->total_bytes;
+    plan->total_bytes += (kv.second.device_bytes + 255) / 256 * 256;
     plan->names.push_back(kv.first);
   }
-  plan->total_bytes = total;
-  plan->layers = layers;
   return plan;
 }
 

@@ -132,7 +132,7 @@ def test_missing_or_malformed_block_tensors_are_refused(tmp_path):
     odd["blocks.0.mlp.up.weight_scale"] = odd["blocks.0.mlp.up.weight_scale"][:250]
     path = tmp_path / "odd.safetensors"
     write_safetensors(path, odd)
-    with Checkpoint(path) as f, pytest.raises(k2.InvalidArgument, match="interleave shape in blocks.0.gu"):
+    with Checkpoint(path) as f, pytest.raises(k2.InvalidArgument, match="blocks.0.gu takes its parts 16 rows at a time in turn"):
         Plan(f)
     path = tmp_path / "empty.safetensors"
     write_safetensors(path, {"x": np.zeros(4, np.float32)})
