@@ -123,6 +123,17 @@ SHAPES = [
     # the streaming kernel past 32 tokens (short K, grid resident at once): two token
     # groups of 64 and 36
     (100, 1024, 4096, 64),
+    # the epilogue stages its output in a stage buffer free at the end of the K loop:
+    # stage 1 after a single K step, stage (steps - 2) mod stages after more; one, two
+    # and three steps on the 64x64 tiles of two K groups, the 128x64 tiles (three
+    # stages), the three-stage 256x128 tiles and the two-stage 256x256 tiles
+    (256, 128, 4096, 0),
+    (256, 256, 4096, 64),
+    (512, 128, 4096, 0),
+    (512, 384, 4096, 64),
+    (200, 128, 19456, 0),
+    (200, 384, 19456, 0),
+    (2000, 384, 8192, 0),
     # the largest K (65536): 128 K steps per wave in the few-token kernel; split K over
     # 128 slices in the tile kernels
     (3, 65536, 512, 0),
