@@ -213,7 +213,9 @@ int k2w8_gemm_i8_noalloc(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, cons
  * K2W8_LINEAR_ONE_LAUNCH=1, the wide-tile shapes (whole rounds of 256x256 or 256x192
  * tiles, width <= 3072) run instead in one persistent launch with a grid-wide barrier
  * between the phases (one workgroup per CU); it gives the same bits but measured
- * slower, so it is not the default.
+ * slower, so it is not the default. That form needs all of its workgroups resident at
+ * once: it must not overlap another one-launch call on the device (concurrent streams),
+ * or its barrier waits until a bounded poll gives up and the results are wrong.
  */
 int k2w8_linear_norm_i8(void *stream, const k2w8_prepare_norm_cfg *cfg, const k2w8_gemm_cfg *gemm,
                         int64_t tokens, const void *h, const float *norm_scale,
