@@ -226,6 +226,30 @@ int k2w8_linear_plain_i8(void *stream, const k2w8_prepare_plain_cfg *cfg, const 
                          const int8_t *w, const float *scale, void *c);
 
 /*
+ * The block's other prepare -> GEMM pairs as one call each (always two launches),
+ * with the arguments of the two entry points they chain and the same bits:
+ *   linear_gated_resid_i8: prepare_gated_i8 -> gemm_i8_resid (the attention output
+ *     projection, src/session/mod.rs:757-783);
+ *   linear_norm_swiglu_i8: prepare_norm_i8 -> gemm_i8_swiglu (gate|up,
+ *     src/session/mod.rs:785-813);
+ *   linear_plain_resid_i8: prepare_plain_i8 -> gemm_i8_resid (down,
+ *     src/session/mod.rs:815-840).
+ * `gate_in` is the gated prepare's gate, `gate` the residual's per-channel gate, `x`
+ * the bf16 residual updated in place.
+ */
+int k2w8_linear_gated_resid_i8(void *stream, const k2w8_prepare_gated_cfg *cfg, const k2w8_gemm_cfg *gemm,
+                               int64_t tokens, const void *attn, const void *gate_in, int8_t *q,
+                               float *q_scale, const int8_t *w, const float *scale, void *x,
+                               const float *gate);
+int k2w8_linear_norm_swiglu_i8(void *stream, const k2w8_prepare_norm_cfg *cfg, const k2w8_gemm_cfg *gemm,
+                               int64_t tokens, const void *h, const float *norm_scale,
+                               const float *mod_scale, const float *mod_shift, int8_t *q,
+                               float *q_scale, const int8_t *w, const float *scale, void *c);
+int k2w8_linear_plain_resid_i8(void *stream, const k2w8_prepare_plain_cfg *cfg, const k2w8_gemm_cfg *gemm,
+                               int64_t tokens, const void *h, int8_t *q, float *q_scale,
+                               const int8_t *w, const float *scale, void *x, const float *gate);
+
+/*
  * lora_transport: replaces krea2_lora_transport (kernels/native/lora_transport.loom:5-41),
  * the 16-bit format change around the W8A8 projection of src/training/quantized.rs:66-105.
  * Each element is widened exactly to f32 and rounded (nearest even) to the other format.

@@ -212,60 +212,99 @@ int k2w8_prepare_plain_i8(void *stream, const k2w8_prepare_plain_cfg *cfg, int64
 
 // Fused prepare -> gemm_i8: validate both halves as their own entry points do, run the
 // one-launch form where it exists for the shape, else the two launches.
-static int run_linear(const char *stage, int kind, void *stream, int64_t width, int64_t out_stride,
-                      float eps, const k2w8_gemm_cfg *gcfg, int64_t tokens, const void *h,
-                      const float *norm_scale, const float *mod_scale, const float *mod_shift,
-                      int8_t *q, float *q_scale, const int8_t *w, const float *scale, void *c) {
+// A prepare (kind 0 norm, 1 plain, 2 gated) and the GEMM that reads its q / q_scale,
+// with the given epilogue. Both halves are validated before either launches.
+struct LinearPrepare {
+  int kind;
+  int64_t width, out_stride, gate_stride;
+  float eps;
+  const void *h, *gate_in;
+  const float *norm_scale, *mod_scale, *mod_shift;
+};
+
+static int run_linear(const char *stage, const LinearPrepare &lp, int epi, void *stream,
+                      const k2w8_gemm_cfg *gcfg, int64_t tokens, int8_t *q, float *q_scale,
+                      const int8_t *w, const float *scale, void *c, const float *gate) {
   if (!gcfg) return fail(K2W8_INVALID_ARGUMENT, "%s: null configuration", stage);
-  int rc = check_prepare(stage, tokens, width, out_stride, h, q, q_scale);
+  int rc = check_prepare(stage, tokens, lp.width, lp.out_stride, lp.h, q, q_scale);
   if (rc != K2W8_OK) return rc;
   if ((rc = check_gemm(stage, gcfg, tokens, q, w, scale, q_scale, c)) != K2W8_OK) return rc;
-  if (gcfg->k_size != width || gcfg->k_stride != out_stride)
+  if (gcfg->k_size != lp.width || gcfg->k_stride != lp.out_stride)
     return fail(K2W8_INVALID_ARGUMENT,
                 "%s: the GEMM's k_size and k_stride must be the prepare's width and out_stride", stage);
-  if (kind == 0) {
-    if (!norm_scale || !mod_scale || !mod_shift)
+  if (lp.kind == 0) {
+    if (!lp.norm_scale || !lp.mod_scale || !lp.mod_shift)
       return fail(K2W8_INVALID_ARGUMENT, "%s: null norm or modulation vector", stage);
-    if (!aligned(norm_scale, 16) || !aligned(mod_scale, 16) || !aligned(mod_shift, 16))
+    if (!aligned(lp.norm_scale, 16) || !aligned(lp.mod_scale, 16) || !aligned(lp.mod_shift, 16))
       return fail(K2W8_INVALID_ARGUMENT, "%s: norm and modulation vectors must be 16-byte aligned", stage);
-    if (!(eps >= 0.0f)) return fail(K2W8_INVALID_ARGUMENT, "%s: eps must be >= 0", stage);
+    if (!(lp.eps >= 0.0f)) return fail(K2W8_INVALID_ARGUMENT, "%s: eps must be >= 0", stage);
   }
+  if (lp.kind == 2) {
+    if (!lp.gate_in) return fail(K2W8_INVALID_ARGUMENT, "%s: null gate", stage);
+    if (lp.gate_stride < lp.width || lp.gate_stride > 65536 || lp.gate_stride % 8 != 0)
+      return fail(K2W8_INVALID_ARGUMENT, "%s: gate_stride must be a multiple of 8 in width..65536, got %lld",
+                  stage, (long long)lp.gate_stride);
+    if (!aligned(lp.gate_in, 16)) return fail(K2W8_INVALID_ARGUMENT, "%s: gate must be 16-byte aligned", stage);
+  }
+  if (epi == k2w8::kEpiResid && !gate) return fail(K2W8_INVALID_ARGUMENT, "%s: null residual gate", stage);
+  if (gate && !aligned(gate, 16))
+    return fail(K2W8_INVALID_ARGUMENT, "%s: the residual gate must be 16-byte aligned", stage);
   if ((rc = ensure_configured(stage)) != K2W8_OK) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (lp.kind == 2) {
+    hipError_t e = k2w8::prepare_gated_ready(s);
+    if (e == hipErrorStreamCaptureUnsupported)
+      return fail(K2W8_RUNTIME, "%s: the first gated call on a device must not be inside a stream capture "
+                  "(k2w8_prime_launches sets the device up beforehand)", stage);
+    if (e != hipSuccess) return runtime(stage, e);
+  }
   k2w8::PrepareLaunch p;
-  p.h = h;
-  p.norm_scale = norm_scale;
-  p.mod_scale = mod_scale;
-  p.mod_shift = mod_shift;
+  p.h = lp.h;
+  p.gate = lp.gate_in;
+  p.norm_scale = lp.norm_scale;
+  p.mod_scale = lp.mod_scale;
+  p.mod_shift = lp.mod_shift;
   p.q = q;
   p.q_scale = q_scale;
-  p.width = width;
-  p.out_stride = out_stride;
-  p.eps = eps;
+  p.width = lp.width;
+  p.out_stride = lp.out_stride;
+  p.gate_stride = lp.gate_stride;
+  p.eps = lp.eps;
   k2w8::GemmLaunch l;
   l.a = q;
   l.w = w;
   l.w_scale = scale;
   l.a_scale = q_scale;
   l.c = c;
+  l.gate = gate;
   l.m = tokens;
   l.n = gcfg->n_size;
   l.k = gcfg->k_size;
   l.lda = gcfg->k_stride;
   l.m_group = (int)gcfg->m_group;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  // Two launches by default: the one-launch form measured slower (configs[1] 135 ->
-  // 148 us: its prepare phase runs at one workgroup per CU, and the grid barrier's
-  // agent-scope release and acquire write back and invalidate each XCD's L2). Setting
-  // K2W8_LINEAR_ONE_LAUNCH=1 selects it (read on every call).
+  // Two launches by default: the one-launch form (norm or plain prepare, plain
+  // epilogue) measured slower (configs[1] 135 -> 148 us: its prepare phase runs at one
+  // workgroup per CU, and the grid barrier's agent-scope release and acquire write
+  // back and invalidate each XCD's L2). Setting K2W8_LINEAR_ONE_LAUNCH=1 selects it
+  // (read on every call).
   const char *one = getenv("K2W8_LINEAR_ONE_LAUNCH");
-  hipError_t e = (one && one[0] == '1') ? k2w8::launch_prepare_gemm(kind, s, tokens, p, l)
-                                        : hipErrorNotSupported;
+  hipError_t e = (one && one[0] == '1' && lp.kind != 2 && epi == k2w8::kEpiPlain)
+                     ? k2w8::launch_prepare_gemm(lp.kind, s, tokens, p, l)
+                     : hipErrorNotSupported;
   if (e == hipErrorNotSupported) {
-    e = k2w8::launch_prepare(kind, s, tokens, p);
-    if (e == hipSuccess) e = k2w8::launch_gemm(k2w8::kEpiPlain, s, l);
+    e = k2w8::launch_prepare(lp.kind, s, tokens, p);
+    if (e == hipSuccess) e = k2w8::launch_gemm(epi, s, l);
   }
   if (e != hipSuccess) return runtime(stage, e);
   return ok();
+}
+
+static LinearPrepare norm_prepare(const k2w8_prepare_norm_cfg *cfg, const void *h, const float *ns,
+                                  const float *ms, const float *sh) {
+  return LinearPrepare{0, cfg->width, cfg->out_stride, 0, cfg->eps, h, nullptr, ns, ms, sh};
+}
+static LinearPrepare plain_prepare(const k2w8_prepare_plain_cfg *cfg, const void *h) {
+  return LinearPrepare{1, cfg->width, cfg->out_stride, 0, 0.0f, h, nullptr, nullptr, nullptr, nullptr};
 }
 
 int k2w8_linear_norm_i8(void *stream, const k2w8_prepare_norm_cfg *cfg, const k2w8_gemm_cfg *gemm,
@@ -273,16 +312,44 @@ int k2w8_linear_norm_i8(void *stream, const k2w8_prepare_norm_cfg *cfg, const k2
                         const float *mod_scale, const float *mod_shift, int8_t *q,
                         float *q_scale, const int8_t *w, const float *scale, void *c) {
   if (!cfg) return fail(K2W8_INVALID_ARGUMENT, "linear_norm_i8: null configuration");
-  return run_linear("linear_norm_i8", 0, stream, cfg->width, cfg->out_stride, cfg->eps, gemm,
-                    tokens, h, norm_scale, mod_scale, mod_shift, q, q_scale, w, scale, c);
+  return run_linear("linear_norm_i8", norm_prepare(cfg, h, norm_scale, mod_scale, mod_shift), k2w8::kEpiPlain,
+                    stream, gemm, tokens, q, q_scale, w, scale, c, nullptr);
 }
 
 int k2w8_linear_plain_i8(void *stream, const k2w8_prepare_plain_cfg *cfg, const k2w8_gemm_cfg *gemm,
                          int64_t tokens, const void *h, int8_t *q, float *q_scale,
                          const int8_t *w, const float *scale, void *c) {
   if (!cfg) return fail(K2W8_INVALID_ARGUMENT, "linear_plain_i8: null configuration");
-  return run_linear("linear_plain_i8", 1, stream, cfg->width, cfg->out_stride, 0.0f, gemm, tokens,
-                    h, nullptr, nullptr, nullptr, q, q_scale, w, scale, c);
+  return run_linear("linear_plain_i8", plain_prepare(cfg, h), k2w8::kEpiPlain, stream, gemm, tokens, q,
+                    q_scale, w, scale, c, nullptr);
+}
+
+int k2w8_linear_gated_resid_i8(void *stream, const k2w8_prepare_gated_cfg *cfg, const k2w8_gemm_cfg *gemm,
+                               int64_t tokens, const void *attn, const void *gate_in, int8_t *q,
+                               float *q_scale, const int8_t *w, const float *scale, void *x,
+                               const float *gate) {
+  if (!cfg) return fail(K2W8_INVALID_ARGUMENT, "linear_gated_resid_i8: null configuration");
+  const LinearPrepare lp{2, cfg->width, cfg->out_stride, cfg->gate_stride, 0.0f, attn, gate_in,
+                         nullptr, nullptr, nullptr};
+  return run_linear("linear_gated_resid_i8", lp, k2w8::kEpiResid, stream, gemm, tokens, q, q_scale, w, scale,
+                    x, gate);
+}
+
+int k2w8_linear_norm_swiglu_i8(void *stream, const k2w8_prepare_norm_cfg *cfg, const k2w8_gemm_cfg *gemm,
+                               int64_t tokens, const void *h, const float *norm_scale,
+                               const float *mod_scale, const float *mod_shift, int8_t *q,
+                               float *q_scale, const int8_t *w, const float *scale, void *c) {
+  if (!cfg) return fail(K2W8_INVALID_ARGUMENT, "linear_norm_swiglu_i8: null configuration");
+  return run_linear("linear_norm_swiglu_i8", norm_prepare(cfg, h, norm_scale, mod_scale, mod_shift),
+                    k2w8::kEpiSwiglu, stream, gemm, tokens, q, q_scale, w, scale, c, nullptr);
+}
+
+int k2w8_linear_plain_resid_i8(void *stream, const k2w8_prepare_plain_cfg *cfg, const k2w8_gemm_cfg *gemm,
+                               int64_t tokens, const void *h, int8_t *q, float *q_scale,
+                               const int8_t *w, const float *scale, void *x, const float *gate) {
+  if (!cfg) return fail(K2W8_INVALID_ARGUMENT, "linear_plain_resid_i8: null configuration");
+  return run_linear("linear_plain_resid_i8", plain_prepare(cfg, h), k2w8::kEpiResid, stream, gemm, tokens,
+                    q, q_scale, w, scale, x, gate);
 }
 
 int k2w8_prepare_gated_i8(void *stream, const k2w8_prepare_gated_cfg *cfg, int64_t tokens,

@@ -26,8 +26,11 @@ from .ops import (  # noqa: F401
     gemm_i8_swiglu,
     gemm_set_workspace,
     gemm_workspace_bytes,
+    linear_gated_resid_i8,
     linear_norm_i8,
+    linear_norm_swiglu_i8,
     linear_plain_i8,
+    linear_plain_resid_i8,
     lora_transport,
     sigmoid_f32,
     prepare_gated_i8,
@@ -54,8 +57,11 @@ __all__ = [
     "gemm_set_workspace",
     "gemm_workspace_bytes",
     "lib",
+    "linear_gated_resid_i8",
     "linear_norm_i8",
+    "linear_norm_swiglu_i8",
     "linear_plain_i8",
+    "linear_plain_resid_i8",
     "library_path",
     "lora_transport",
     "sigmoid_f32",

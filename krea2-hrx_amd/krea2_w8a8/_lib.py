@@ -156,6 +156,21 @@ SIGNATURES = {
         ctypes.c_int,
         [_P, ctypes.POINTER(PreparePlainCfg), ctypes.POINTER(GemmCfg), _I64, _P, _P, _P, _P, _P, _P],
     ),
+    "k2w8_linear_gated_resid_i8": (
+        ctypes.c_int,
+        [_P, ctypes.POINTER(PrepareGatedCfg), ctypes.POINTER(GemmCfg), _I64, _P, _P, _P, _P, _P, _P, _P,
+         _P],
+    ),
+    "k2w8_linear_norm_swiglu_i8": (
+        ctypes.c_int,
+        [_P, ctypes.POINTER(PrepareNormCfg), ctypes.POINTER(GemmCfg), _I64, _P, _P, _P, _P, _P, _P,
+         _P, _P, _P],
+    ),
+    "k2w8_linear_plain_resid_i8": (
+        ctypes.c_int,
+        [_P, ctypes.POINTER(PreparePlainCfg), ctypes.POINTER(GemmCfg), _I64, _P, _P, _P, _P, _P, _P,
+         _P],
+    ),
     "k2w8_gemm_i8_noalloc": (ctypes.c_int, [_P, ctypes.POINTER(GemmCfg), _I64, _P, _P, _P, _P, _P]),
     "k2w8_gemm_workspace_bytes": (_I64, []),
     "k2w8_lora_transport": (ctypes.c_int, [_P, ctypes.c_int, _I64, _P, _P]),

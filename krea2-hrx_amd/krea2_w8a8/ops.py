@@ -230,6 +230,70 @@ def linear_plain_i8(h, q, q_scale, w, scale, c, *, cfg: "GemmConfig", tokens=Non
     check(lib().k2w8_linear_plain_i8(_stream(stream), ctypes.byref(pc), ctypes.byref(k), n, *args))
 
 
+def linear_gated_resid_i8(attn, gate_in, q, q_scale, w, scale, x, gate, *, cfg: "GemmConfig",
+                          gate_stride, tokens=None, stream=None):
+    """prepare_gated_i8 of ``attn`` x sigmoid(``gate_in``) into ``q``/``q_scale``, then
+    gemm_i8_resid of ``q`` with ``w`` into the bf16 residual ``x`` (per-channel ``gate``),
+    as one call: the block's attention output projection."""
+    n = _tokens(attn, tokens)
+    width, out_stride = cfg.k_size, cfg.k_stride
+    pc = PrepareGatedCfg(width, out_stride, gate_stride)
+    args = (
+        _buf(attn, "attn", torch.float16, n * width),
+        _buf(gate_in, "gate_in", torch.float16, (n - 1) * gate_stride + width),
+        _buf(q, "q", torch.int8, (n - 1) * out_stride + width),
+        _buf(q_scale, "q_scale", torch.float32, n),
+        _buf(w, "w", torch.int8, (cfg.n_size - 1) * cfg.k_stride + cfg.k_size),
+        _buf(scale, "scale", torch.float32, cfg.n_size),
+        _buf(x, "x", torch.bfloat16, n * cfg.n_size),
+        _buf(gate, "gate", torch.float32, cfg.n_size),
+    )
+    k = cfg.c()
+    check(lib().k2w8_linear_gated_resid_i8(_stream(stream), ctypes.byref(pc), ctypes.byref(k), n, *args))
+
+
+def linear_norm_swiglu_i8(h, norm_scale, mod_scale, mod_shift, q, q_scale, w, scale, c, *,
+                          cfg: "GemmConfig", eps, tokens=None, stream=None):
+    """prepare_norm_i8 of ``h`` into ``q``/``q_scale``, then gemm_i8_swiglu into ``c``
+    (f16 [tokens][n/2]), as one call: the block's gate|up projection."""
+    n = _tokens(h, tokens)
+    width, out_stride = cfg.k_size, cfg.k_stride
+    pc = PrepareNormCfg(width, out_stride, eps)
+    args = (
+        _buf(h, "h", torch.bfloat16, n * width),
+        _buf(norm_scale, "norm_scale", torch.float32, width),
+        _buf(mod_scale, "mod_scale", torch.float32, width),
+        _buf(mod_shift, "mod_shift", torch.float32, width),
+        _buf(q, "q", torch.int8, (n - 1) * out_stride + width),
+        _buf(q_scale, "q_scale", torch.float32, n),
+        _buf(w, "w", torch.int8, (cfg.n_size - 1) * cfg.k_stride + cfg.k_size),
+        _buf(scale, "scale", torch.float32, cfg.n_size),
+        _buf(c, "c", torch.float16, n * (cfg.n_size // 2)),
+    )
+    k = cfg.c()
+    check(lib().k2w8_linear_norm_swiglu_i8(_stream(stream), ctypes.byref(pc), ctypes.byref(k), n, *args))
+
+
+def linear_plain_resid_i8(h, q, q_scale, w, scale, x, gate, *, cfg: "GemmConfig", tokens=None,
+                          stream=None):
+    """prepare_plain_i8 of f16 ``h`` into ``q``/``q_scale``, then gemm_i8_resid into the
+    bf16 residual ``x`` (per-channel ``gate``), as one call: the block's down projection."""
+    n = _tokens(h, tokens)
+    width, out_stride = cfg.k_size, cfg.k_stride
+    pc = PreparePlainCfg(width, out_stride)
+    args = (
+        _buf(h, "h", torch.float16, n * width),
+        _buf(q, "q", torch.int8, (n - 1) * out_stride + width),
+        _buf(q_scale, "q_scale", torch.float32, n),
+        _buf(w, "w", torch.int8, (cfg.n_size - 1) * cfg.k_stride + cfg.k_size),
+        _buf(scale, "scale", torch.float32, cfg.n_size),
+        _buf(x, "x", torch.bfloat16, n * cfg.n_size),
+        _buf(gate, "gate", torch.float32, cfg.n_size),
+    )
+    k = cfg.c()
+    check(lib().k2w8_linear_plain_resid_i8(_stream(stream), ctypes.byref(pc), ctypes.byref(k), n, *args))
+
+
 def gemm_set_workspace(workspace, *, stream=None):
     """Hand the GEMMs on ``stream`` (default: torch's current stream) a caller-owned
     split-K workspace (a device tensor; its bytes are used, its dtype is not), or remove

@@ -110,3 +110,74 @@ def test_back_to_back_calls_and_graph_replays(mode):
         torch.cuda.synchronize()
         assert torch.equal(og.view(torch.int16), want.view(torch.int16)), replay
         assert torch.equal(qg, q), replay
+
+
+PAIRS = [
+    # (pair, tokens, width, n): the block's projections at a small and a ragged size
+    ("gated_resid", 300, 1024, 1024),
+    ("gated_resid", 77, 3072, 3072),
+    ("norm_swiglu", 300, 1024, 4096),
+    ("norm_swiglu", 513, 2048, 8192),
+    ("plain_resid", 300, 4096, 1024),
+    ("plain_resid", 256, 9728, 2560),  # the down projection that splits K
+]
+
+
+@pytest.mark.parametrize("pair,m,k,n", PAIRS)
+def test_block_pairs_equal_their_two_entry_points(pair, m, k, n):
+    rng = np.random.default_rng(m * 3 + k + n)
+    x = activations(rng, m, k)
+    w = dev(int8_weights(rng, n, k))
+    ws = dev(channel_scales(rng, n))
+    cfg = k2.GemmConfig(k_size=k, n_size=n, k_stride=k)
+    if pair == "gated_resid":
+        attn = dev(f16_bits(x), torch.float16)
+        g_in = dev(f16_bits(rng.standard_normal((m, k)).astype(np.float32)), torch.float16)
+        gate = dev(rng.uniform(0.5, 1.5, n).astype(np.float32))
+        x0 = dev(bf16_bits(rng.standard_normal(m * n).astype(np.float32)), torch.bfloat16)
+        res = []
+        for fused in (True, False):
+            q = torch.full((m, k), 91, dtype=torch.int8, device="cuda")
+            s = torch.zeros(m, dtype=torch.float32, device="cuda")
+            xx = x0.clone()
+            if fused:
+                k2.linear_gated_resid_i8(attn, g_in, q, s, w, ws, xx, gate, cfg=cfg, gate_stride=k)
+            else:
+                k2.prepare_gated_i8(attn, g_in, q, s, width=k, out_stride=k, gate_stride=k)
+                k2.gemm_i8_resid(q, w, ws, s, xx, gate, cfg=cfg)
+            res.append((q, s, xx))
+    elif pair == "norm_swiglu":
+        h = dev(bf16_bits(x), torch.bfloat16)
+        ns = dev((rng.uniform(0.5, 1.5, k) - 1.0).astype(np.float32))
+        ms = dev((rng.uniform(-0.2, 0.2, k)).astype(np.float32))
+        sh = dev((rng.uniform(-0.1, 0.1, k)).astype(np.float32))
+        res = []
+        for fused in (True, False):
+            q = torch.full((m, k), 91, dtype=torch.int8, device="cuda")
+            s = torch.zeros(m, dtype=torch.float32, device="cuda")
+            c = torch.zeros((m, n // 2), dtype=torch.float16, device="cuda")
+            if fused:
+                k2.linear_norm_swiglu_i8(h, ns, ms, sh, q, s, w, ws, c, cfg=cfg, eps=1e-6)
+            else:
+                k2.prepare_norm_i8(h, ns, ms, sh, q, s, width=k, out_stride=k, eps=1e-6)
+                k2.gemm_i8_swiglu(q, w, ws, s, c, cfg=cfg)
+            res.append((q, s, c))
+    else:
+        h = dev(f16_bits(x), torch.float16)
+        gate = dev(rng.uniform(0.5, 1.5, n).astype(np.float32))
+        x0 = dev(bf16_bits(rng.standard_normal(m * n).astype(np.float32)), torch.bfloat16)
+        res = []
+        for fused in (True, False):
+            q = torch.full((m, k), 91, dtype=torch.int8, device="cuda")
+            s = torch.zeros(m, dtype=torch.float32, device="cuda")
+            xx = x0.clone()
+            if fused:
+                k2.linear_plain_resid_i8(h, q, s, w, ws, xx, gate, cfg=cfg)
+            else:
+                k2.prepare_plain_i8(h, q, s, width=k, out_stride=k)
+                k2.gemm_i8_resid(q, w, ws, s, xx, gate, cfg=cfg)
+            res.append((q, s, xx))
+    torch.cuda.synchronize()
+    (q1, s1, o1), (q2, s2, o2) = res
+    assert torch.equal(q1, q2) and torch.equal(s1, s2)
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
