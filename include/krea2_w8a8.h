@@ -522,6 +522,20 @@ int k2w8_blocks_profile(void *stream, const k2w8_block_cfg *cfg, int64_t layers,
 int64_t k2w8_block_stage_count(void);
 const char *k2w8_block_stage_label(int64_t index);
 
+/*
+ * Configuration checks alone, as the reference's config.decl ranges constrain each
+ * kernel (kernels/gemm_i8_256.loom:14-22, kernels/prepare_norm_i8.loom:11-16,
+ * kernels/prepare_plain_i8.loom:10-13, kernels/prepare_gated_i8.loom:11-16): K2W8_OK,
+ * or K2W8_INVALID_ARGUMENT with the reason in k2w8_last_error(). The entry points run
+ * the same checks. Every configuration the reference accepts passes, except GEMM
+ * k_size values that are odd multiples of 64 (this build's K step is 128 bytes; no
+ * production shape has one) and a gated gate_stride below the width.
+ */
+int k2w8_validate_gemm_cfg(const k2w8_gemm_cfg *cfg);
+int k2w8_validate_prepare_norm_cfg(const k2w8_prepare_norm_cfg *cfg);
+int k2w8_validate_prepare_plain_cfg(const k2w8_prepare_plain_cfg *cfg);
+int k2w8_validate_prepare_gated_cfg(const k2w8_prepare_gated_cfg *cfg);
+
 /* Launch-shape rules of src/kernels/shape.rs:7-112. */
 int64_t k2w8_shape_gemm_pitch(int64_t k);    /* shape.rs:105-107 */
 int64_t k2w8_shape_capacity(int64_t tokens); /* shape.rs:12-16 */

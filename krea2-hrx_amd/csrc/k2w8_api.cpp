@@ -58,6 +58,18 @@ bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 // Token bound of the prepares and GEMMs (kernels/prepare_norm_i8.loom:56, gemm m range).
 constexpr int64_t kMaxTokens = 1 << 20;
 
+int check_prepare_shape(const char *stage, int64_t width, int64_t out_stride) {
+  if (width < 256 || width > 32768 || width % 256 != 0)
+    return fail(K2W8_INVALID_ARGUMENT,
+                "%s: width must be a multiple of 256 in 256..32768, got %lld", stage,
+                (long long)width);
+  if (out_stride < width || out_stride > 65536 || out_stride % 64 != 0)
+    return fail(K2W8_INVALID_ARGUMENT,
+                "%s: out_stride must be a multiple of 64 in width..65536, got %lld", stage,
+                (long long)out_stride);
+  return K2W8_OK;
+}
+
 int check_prepare(const char *stage, int64_t tokens, int64_t width, int64_t out_stride,
                   const void *h, const int8_t *q, const float *q_scale) {
   if (tokens < 1 || tokens > kMaxTokens)
@@ -77,9 +89,7 @@ int check_prepare(const char *stage, int64_t tokens, int64_t width, int64_t out_
   return K2W8_OK;
 }
 
-int check_gemm(const char *stage, const k2w8_gemm_cfg *cfg, int64_t m, const int8_t *a,
-               const int8_t *w, const float *scale, const float *a_scale, const void *c) {
-  if (!cfg) return fail(K2W8_INVALID_ARGUMENT, "%s: null configuration", stage);
+int check_gemm_cfg(const char *stage, const k2w8_gemm_cfg *cfg) {
   if (cfg->k_size < 128 || cfg->k_size > 65536 || cfg->k_size % 128 != 0)
     return fail(K2W8_INVALID_ARGUMENT, "%s: k_size must be a multiple of 128 in 128..65536, got %lld",
                 stage, (long long)cfg->k_size);
@@ -92,6 +102,17 @@ int check_gemm(const char *stage, const k2w8_gemm_cfg *cfg, int64_t m, const int
   if (cfg->m_group < 1 || cfg->m_group > 4)
     return fail(K2W8_INVALID_ARGUMENT, "%s: m_group must be 1..4, got %lld", stage,
                 (long long)cfg->m_group);
+  if (cfg->schedule_rows < 0 || cfg->schedule_rows > 1)
+    return fail(K2W8_INVALID_ARGUMENT, "%s: schedule_rows must be 0 or 1, got %lld", stage,
+                (long long)cfg->schedule_rows);
+  return K2W8_OK;
+}
+
+int check_gemm(const char *stage, const k2w8_gemm_cfg *cfg, int64_t m, const int8_t *a,
+               const int8_t *w, const float *scale, const float *a_scale, const void *c) {
+  if (!cfg) return fail(K2W8_INVALID_ARGUMENT, "%s: null configuration", stage);
+  int rc = check_gemm_cfg(stage, cfg);
+  if (rc != K2W8_OK) return rc;
   if (m < 1 || m > 16777216)
     return fail(K2W8_INVALID_ARGUMENT, "%s: m must be 1..16777216, got %lld", stage, (long long)m);
   // 32-bit element offsets inside the kernels.
@@ -631,6 +652,44 @@ int k2w8_quantized_forward(void *stream, const k2w8_quantized_cfg *cfg, int64_t 
 }
 
 // src/kernels/shape.rs:105-107
+// Configuration checks alone, as the reference's config.decl ranges constrain each
+// kernel's specialisation (kernels/gemm_i8_256.loom:14-22,
+// kernels/prepare_norm_i8.loom:11-16, kernels/prepare_plain_i8.loom:10-13,
+// kernels/prepare_gated_i8.loom:11-16): a caller can check a configuration once, before
+// it records or launches anything. The entry points run the same checks.
+int k2w8_validate_gemm_cfg(const k2w8_gemm_cfg *cfg) {
+  if (!cfg) return fail(K2W8_INVALID_ARGUMENT, "validate_gemm_cfg: null configuration");
+  const int rc = check_gemm_cfg("validate_gemm_cfg", cfg);
+  return rc != K2W8_OK ? rc : ok();
+}
+
+int k2w8_validate_prepare_norm_cfg(const k2w8_prepare_norm_cfg *cfg) {
+  const char *stage = "validate_prepare_norm_cfg";
+  if (!cfg) return fail(K2W8_INVALID_ARGUMENT, "%s: null configuration", stage);
+  const int rc = check_prepare_shape(stage, cfg->width, cfg->out_stride);
+  if (rc != K2W8_OK) return rc;
+  if (!(cfg->eps >= 0.0f)) return fail(K2W8_INVALID_ARGUMENT, "%s: eps must be >= 0", stage);
+  return ok();
+}
+
+int k2w8_validate_prepare_plain_cfg(const k2w8_prepare_plain_cfg *cfg) {
+  const char *stage = "validate_prepare_plain_cfg";
+  if (!cfg) return fail(K2W8_INVALID_ARGUMENT, "%s: null configuration", stage);
+  const int rc = check_prepare_shape(stage, cfg->width, cfg->out_stride);
+  return rc != K2W8_OK ? rc : ok();
+}
+
+int k2w8_validate_prepare_gated_cfg(const k2w8_prepare_gated_cfg *cfg) {
+  const char *stage = "validate_prepare_gated_cfg";
+  if (!cfg) return fail(K2W8_INVALID_ARGUMENT, "%s: null configuration", stage);
+  const int rc = check_prepare_shape(stage, cfg->width, cfg->out_stride);
+  if (rc != K2W8_OK) return rc;
+  if (cfg->gate_stride < cfg->width || cfg->gate_stride > 65536 || cfg->gate_stride % 8 != 0)
+    return fail(K2W8_INVALID_ARGUMENT, "%s: gate_stride must be a multiple of 8 in width..65536, got %lld",
+                stage, (long long)cfg->gate_stride);
+  return ok();
+}
+
 int64_t k2w8_shape_gemm_pitch(int64_t k) { return (k % 8192 == 0) ? k + 64 : k; }
 
 // src/kernels/shape.rs:12-16

@@ -221,6 +221,10 @@ SIGNATURES = {
     "k2w8_shape_capacity": (_I64, [_I64]),
     "k2w8_shape_gemm_grid_rows": (_I64, [_I64]),
     "k2w8_shape_gemm_schedule_rows": (ctypes.c_int, [_I64]),
+    "k2w8_validate_gemm_cfg": (ctypes.c_int, [ctypes.POINTER(GemmCfg)]),
+    "k2w8_validate_prepare_norm_cfg": (ctypes.c_int, [ctypes.POINTER(PrepareNormCfg)]),
+    "k2w8_validate_prepare_plain_cfg": (ctypes.c_int, [ctypes.POINTER(PreparePlainCfg)]),
+    "k2w8_validate_prepare_gated_cfg": (ctypes.c_int, [ctypes.POINTER(PrepareGatedCfg)]),
     "k2w8_shape_gemm_rows": (_I64, []),
     "k2w8_shape_gemm_m_group": (_I64, []),
     "k2w8_shape_tokens_min": (_I64, []),

@@ -242,3 +242,31 @@ def test_block_attention_needs_its_workspaces_and_a_head_ratio(k2):
     short = k2._lib.BlockCfg(8, 3072, 12288, 9216, 6144, 1e-5)
     assert L.k2w8_block_attention(None, ctypes.byref(short), 0, ctypes.byref(w), ctypes.byref(b)) == -1
     assert "tokens" in L.k2w8_last_error().decode()
+
+
+def test_config_validators_accept_the_reference_ranges_and_name_what_they_reject(k2):
+    L = k2._lib
+    lib = k2.lib()
+    ok = L.K2W8_OK if hasattr(L, "K2W8_OK") else 0
+    # every production configuration passes (hidden 6144 / 3072, intermediate 16384 at
+    # pitch 16448, the gate half of the fused output at stride 15360)
+    for k, n, stride in [(6144, 15360, 6144), (16384, 6144, 16448), (3072, 9216, 3072), (9728, 2560, 9728)]:
+        assert lib.k2w8_validate_gemm_cfg(ctypes.byref(L.GemmCfg(k, n, stride, 4, 1))) == ok
+    assert lib.k2w8_validate_prepare_norm_cfg(ctypes.byref(L.PrepareNormCfg(6144, 6144, 1e-5))) == ok
+    assert lib.k2w8_validate_prepare_plain_cfg(ctypes.byref(L.PreparePlainCfg(16384, 16448))) == ok
+    assert lib.k2w8_validate_prepare_gated_cfg(ctypes.byref(L.PrepareGatedCfg(6144, 6144, 15360))) == ok
+    bad = [
+        (lib.k2w8_validate_gemm_cfg, L.GemmCfg(3000, 3072, 3072, 4, 0), "k_size"),
+        (lib.k2w8_validate_gemm_cfg, L.GemmCfg(3072, 3000, 3072, 4, 0), "n_size"),
+        (lib.k2w8_validate_gemm_cfg, L.GemmCfg(3072, 3072, 3008, 4, 0), "k_stride"),
+        (lib.k2w8_validate_gemm_cfg, L.GemmCfg(3072, 3072, 3072, 5, 0), "m_group"),
+        (lib.k2w8_validate_gemm_cfg, L.GemmCfg(3072, 3072, 3072, 4, 2), "schedule_rows"),
+        (lib.k2w8_validate_prepare_norm_cfg, L.PrepareNormCfg(3000, 3072, 1e-6), "width"),
+        (lib.k2w8_validate_prepare_norm_cfg, L.PrepareNormCfg(3072, 3072, -1.0), "eps"),
+        (lib.k2w8_validate_prepare_plain_cfg, L.PreparePlainCfg(3072, 3000), "out_stride"),
+        (lib.k2w8_validate_prepare_gated_cfg, L.PrepareGatedCfg(3072, 3072, 3068), "gate_stride"),
+    ]
+    for fn, cfg, fragment in bad:
+        assert fn(ctypes.byref(cfg)) == L.K2W8_INVALID_ARGUMENT, fragment
+        assert fragment in lib.k2w8_last_error().decode()
+    assert lib.k2w8_validate_gemm_cfg(None) == L.K2W8_INVALID_ARGUMENT
