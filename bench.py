@@ -44,7 +44,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="headline step only")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
-    p.add_argument("--probe", choices=["north_star", "skinny", "attention"],
+    p.add_argument("--probe", choices=["north_star", "skinny", "attention", "mfma_peak"],
                    help="run one workload a few times and exit (a short program for "
                         "rocprofv3 --pmc counter passes)")
     p.add_argument("--traffic-probe", action="store_true",
@@ -93,6 +93,8 @@ def main():
         args.steps, args.warmup = 3, 1
         if args.probe == "north_star":
             print(json.dumps(north_star(k2, torch, weights, hidden, args)), flush=True)
+        elif args.probe == "mfma_peak":
+            print(json.dumps(mfma_peak(k2, torch)), flush=True)
         elif args.probe == "skinny":
             skinny_sweep(k2, torch, weights, hidden, args, warm=False)
         else:
@@ -294,6 +296,25 @@ def batch_timed(torch, fn, steps, warmup):
     e1.record(stream)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) * 1e-3 / steps
+
+
+def mfma_peak(k2, torch):
+    """The INT8 MFMA rate with nothing but MFMAs running (k2w8_probe_mfma_i8): two waves
+    per SIMD on every CU, register operands of pseudo-random bytes and of bytes of 1.
+    The chip's power limit sets the clock it holds, and the MFMA's power depends on its
+    operand bits: this is the ceiling the tile GEMM is measured against."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    blocks, iters = 2 * cus, 20000
+    out = torch.empty(blocks * 256, dtype=torch.int32, device="cuda")
+    res = {"blocks": blocks, "iters": iters}
+    for name, random in (("random", True), ("ones", False)):
+        def fn(_):
+            k2.probe_mfma_i8(out, blocks=blocks, iters=iters, random=random)
+        sec = event_timed(torch, fn, 5, 2)
+        tops = blocks * iters * float(1 << 21) / sec / 1e12  # 4 waves x 8 MFMAs x 2^16 ops
+        res[name] = {"us": round(sec * 1e6, 1), "TOPS": round(tops, 1),
+                     "pct_of_int8_peak": round(100 * tops / PEAK_INT8_TOPS, 1)}
+    return res
 
 
 def north_star(k2, torch, weights, hidden, args):

@@ -523,6 +523,18 @@ int64_t k2w8_block_stage_count(void);
 const char *k2w8_block_stage_label(int64_t index);
 
 /*
+ * probe_mfma_i8: a measurement aid with no counterpart in the reference. Back-to-back
+ * v_mfma_i32_32x32x32_i8 on operands held in registers (pseudo-random bytes from
+ * `seed` when `random` is non-zero, else bytes of 1), `blocks` workgroups of four waves,
+ * `iters` steps of eight MFMAs per wave: 2^21 * blocks * iters ops. The INT8 MFMA rate
+ * the chip holds under its power limit, which the tile GEMM is measured against.
+ * out: int32 [blocks * 256], each lane's accumulator sum (with bytes of 1:
+ * 4096 * iters).
+ */
+int k2w8_probe_mfma_i8(void *stream, int64_t blocks, int64_t iters, int32_t random, uint32_t seed,
+                       int32_t *out);
+
+/*
  * Configuration checks alone, as the reference's config.decl ranges constrain each
  * kernel (kernels/gemm_i8_256.loom:14-22, kernels/prepare_norm_i8.loom:11-16,
  * kernels/prepare_plain_i8.loom:10-13, kernels/prepare_gated_i8.loom:11-16): K2W8_OK,

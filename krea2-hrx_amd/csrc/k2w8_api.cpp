@@ -652,6 +652,19 @@ int k2w8_quantized_forward(void *stream, const k2w8_quantized_cfg *cfg, int64_t 
 }
 
 // src/kernels/shape.rs:105-107
+// Measurement aid (no reference counterpart): the MFMA-only INT8 rate, k2w8_probe.hip.
+int k2w8_probe_mfma_i8(void *stream, int64_t blocks, int64_t iters, int32_t random, uint32_t seed,
+                       int32_t *out) {
+  const char *stage = "probe_mfma_i8";
+  if (blocks < 1 || blocks > 65536 || iters < 1 || iters > (int64_t(1) << 24))
+    return fail(K2W8_INVALID_ARGUMENT, "%s: blocks must be 1..65536 and iters 1..2^24", stage);
+  if (!out || !aligned(out, 4)) return fail(K2W8_INVALID_ARGUMENT, "%s: null or misaligned out", stage);
+  const hipError_t e = k2w8::launch_probe_mfma(static_cast<hipStream_t>(stream), blocks, iters, random ? 1 : 0,
+                                               seed, out);
+  if (e != hipSuccess) return runtime(stage, e);
+  return ok();
+}
+
 // Configuration checks alone, as the reference's config.decl ranges constrain each
 // kernel's specialisation (kernels/gemm_i8_256.loom:14-22,
 // kernels/prepare_norm_i8.loom:11-16, kernels/prepare_plain_i8.loom:10-13,

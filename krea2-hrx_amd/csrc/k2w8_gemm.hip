@@ -193,7 +193,7 @@ template <int EPI, int BM, int BN>
 __device__ __forceinline__ void stage_epi_operands(const GemmArgs &g, int m0, int n0, int lane,
                                                    uint32_t lds) {
   using E = EpiOperands<BM, BN>;
-  static_assert(BN * 4 <= 1024 && BM % 64 == 0 || BM < 64, "one transfer per column operand");
+  static_assert((BN * 4 <= 1024 && BM % 64 == 0) || BM < 64, "one transfer per column operand");
   if (EPI == kEpiAcc) return;
   if (lane < BN / 4) dma16(lds + E::kWs, reinterpret_cast<const int8_t *>(g.w_scale), (uint32_t)(n0 * 4 + lane * 16));
   if (EPI == kEpiBias && lane < BN / 8)

@@ -61,6 +61,8 @@ hipError_t configure_skinny_lds();
 
 // bf16 <-> f16 transport: direction 1 bf16 -> f16, 2 f16 -> bf16.
 hipError_t launch_sigmoid(hipStream_t stream, int64_t count, const float *x, float *out);
+hipError_t launch_probe_mfma(hipStream_t stream, int64_t blocks, int64_t iters, int random, uint32_t seed,
+                             int32_t *out);
 hipError_t launch_transport(int direction, hipStream_t stream, int64_t count, const void *x,
                             void *out);
 

@@ -31,6 +31,7 @@ from .ops import (  # noqa: F401
     linear_norm_swiglu_i8,
     linear_plain_i8,
     linear_plain_resid_i8,
+    probe_mfma_i8,
     lora_transport,
     sigmoid_f32,
     prepare_gated_i8,
@@ -62,6 +63,7 @@ __all__ = [
     "linear_norm_swiglu_i8",
     "linear_plain_i8",
     "linear_plain_resid_i8",
+    "probe_mfma_i8",
     "library_path",
     "lora_transport",
     "sigmoid_f32",

@@ -221,6 +221,7 @@ SIGNATURES = {
     "k2w8_shape_capacity": (_I64, [_I64]),
     "k2w8_shape_gemm_grid_rows": (_I64, [_I64]),
     "k2w8_shape_gemm_schedule_rows": (ctypes.c_int, [_I64]),
+    "k2w8_probe_mfma_i8": (ctypes.c_int, [_P, _I64, _I64, ctypes.c_int32, ctypes.c_uint32, _P]),
     "k2w8_validate_gemm_cfg": (ctypes.c_int, [ctypes.POINTER(GemmCfg)]),
     "k2w8_validate_prepare_norm_cfg": (ctypes.c_int, [ctypes.POINTER(PrepareNormCfg)]),
     "k2w8_validate_prepare_plain_cfg": (ctypes.c_int, [ctypes.POINTER(PreparePlainCfg)]),

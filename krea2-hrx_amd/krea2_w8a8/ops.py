@@ -439,3 +439,12 @@ class Quantized:
         )
         check(lib().k2w8_quantized_forward(_stream(stream), ctypes.byref(cfg), rows, *args))
         return out
+
+
+def probe_mfma_i8(out, *, blocks, iters, random=True, seed=1, stream=None):
+    """The MFMA-only INT8 rate probe (a measurement aid, not part of the path):
+    ``blocks`` workgroups of four waves run ``iters`` steps of eight back-to-back
+    v_mfma_i32_32x32x32_i8 per wave (2^21 * blocks * iters ops) on register operands,
+    pseudo-random bytes or bytes of 1. ``out`` int32 [blocks * 256]."""
+    o = _buf(out, "out", torch.int32, blocks * 256)
+    check(lib().k2w8_probe_mfma_i8(_stream(stream), blocks, iters, 1 if random else 0, seed, o))

@@ -83,3 +83,20 @@ def test_device_sigmoid_over_every_f32_input():
         assert np.array_equal(np.isnan(got), nan), c
         diff = got.view(np.uint32)[~nan] != want.view(np.uint32)[~nan]
         assert not diff.any(), (c, int(diff.sum()))
+
+
+def test_mfma_probe_counts_every_mfma():
+    # With bytes of 1 every v_mfma_i32_32x32x32_i8 adds 32 to each accumulator: a lane's
+    # eight chains of 16 accumulators sum to 4096 per step. Pseudo-random operands give
+    # the same sums on every run.
+    import krea2_w8a8 as k2
+    out = torch.zeros(3 * 256, dtype=torch.int32, device="cuda")
+    k2.probe_mfma_i8(out, blocks=3, iters=7, random=False)
+    torch.cuda.synchronize()
+    assert torch.all(out == 4096 * 7)
+    a = torch.zeros_like(out)
+    b = torch.zeros_like(out)
+    k2.probe_mfma_i8(a, blocks=3, iters=5, random=True, seed=9)
+    k2.probe_mfma_i8(b, blocks=3, iters=5, random=True, seed=9)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and int(a.abs().sum()) > 0
