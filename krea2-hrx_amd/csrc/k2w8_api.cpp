@@ -75,17 +75,43 @@ int check_prepare(const char *stage, int64_t tokens, int64_t width, int64_t out_
   if (tokens < 1 || tokens > kMaxTokens)
     return fail(K2W8_INVALID_ARGUMENT, "%s: tokens must be 1..%lld, got %lld", stage,
                 (long long)kMaxTokens, (long long)tokens);
-  if (width < 256 || width > 32768 || width % 256 != 0)
-    return fail(K2W8_INVALID_ARGUMENT,
-                "%s: width must be a multiple of 256 in 256..32768, got %lld", stage,
-                (long long)width);
-  if (out_stride < width || out_stride > 65536 || out_stride % 64 != 0)
-    return fail(K2W8_INVALID_ARGUMENT,
-                "%s: out_stride must be a multiple of 64 in width..65536, got %lld", stage,
-                (long long)out_stride);
+  const int rc = check_prepare_shape(stage, width, out_stride);
+  if (rc != K2W8_OK) return rc;
   if (!h || !q || !q_scale) return fail(K2W8_INVALID_ARGUMENT, "%s: null buffer", stage);
   if (!aligned(h, 16) || !aligned(q, 16) || !aligned(q_scale, 4))
     return fail(K2W8_INVALID_ARGUMENT, "%s: h and q must be 16-byte aligned", stage);
+  return K2W8_OK;
+}
+
+// The norm prepare's vectors (kernels/prepare_norm_i8.loom:22) and eps.
+int check_norm_vectors(const char *stage, const float *norm_scale, const float *mod_scale,
+                       const float *mod_shift, float eps) {
+  if (!norm_scale || !mod_scale || !mod_shift)
+    return fail(K2W8_INVALID_ARGUMENT, "%s: null norm or modulation vector", stage);
+  if (!aligned(norm_scale, 16) || !aligned(mod_scale, 16) || !aligned(mod_shift, 16))
+    return fail(K2W8_INVALID_ARGUMENT, "%s: norm and modulation vectors must be 16-byte aligned", stage);
+  if (!(eps >= 0.0f)) return fail(K2W8_INVALID_ARGUMENT, "%s: eps must be >= 0", stage);
+  return K2W8_OK;
+}
+
+// The gated prepare's gate operand and its row stride (kernels/prepare_gated_i8.loom:16).
+int check_gate_input(const char *stage, const void *gate, int64_t width, int64_t gate_stride) {
+  if (!gate) return fail(K2W8_INVALID_ARGUMENT, "%s: null gate", stage);
+  if (gate_stride < width || gate_stride > 65536 || gate_stride % 8 != 0)
+    return fail(K2W8_INVALID_ARGUMENT, "%s: gate_stride must be a multiple of 8 in width..65536, got %lld",
+                stage, (long long)gate_stride);
+  if (!aligned(gate, 16)) return fail(K2W8_INVALID_ARGUMENT, "%s: gate must be 16-byte aligned", stage);
+  return K2W8_OK;
+}
+
+// The gated prepare's sigmoid table is uploaded on the first call on a device, which
+// must not happen inside a stream capture.
+int gated_ready(const char *stage, hipStream_t stream) {
+  const hipError_t e = k2w8::prepare_gated_ready(stream);
+  if (e == hipErrorStreamCaptureUnsupported)
+    return fail(K2W8_RUNTIME, "%s: the first gated call on a device must not be inside a stream capture "
+                "(k2w8_prime_launches sets the device up beforehand)", stage);
+  if (e != hipSuccess) return runtime(stage, e);
   return K2W8_OK;
 }
 
@@ -192,11 +218,7 @@ int k2w8_prepare_norm_i8(void *stream, const k2w8_prepare_norm_cfg *cfg, int64_t
   if (!cfg) return fail(K2W8_INVALID_ARGUMENT, "%s: null configuration", stage);
   int rc = check_prepare(stage, tokens, cfg->width, cfg->out_stride, h, q, q_scale);
   if (rc != K2W8_OK) return rc;
-  if (!norm_scale || !mod_scale || !mod_shift)
-    return fail(K2W8_INVALID_ARGUMENT, "%s: null norm or modulation vector", stage);
-  if (!aligned(norm_scale, 16) || !aligned(mod_scale, 16) || !aligned(mod_shift, 16))
-    return fail(K2W8_INVALID_ARGUMENT, "%s: norm and modulation vectors must be 16-byte aligned", stage);
-  if (!(cfg->eps >= 0.0f)) return fail(K2W8_INVALID_ARGUMENT, "%s: eps must be >= 0", stage);
+  if ((rc = check_norm_vectors(stage, norm_scale, mod_scale, mod_shift, cfg->eps)) != K2W8_OK) return rc;
   if ((rc = ensure_configured(stage)) != K2W8_OK) return rc;
   k2w8::PrepareLaunch p;
   p.h = h;
@@ -231,10 +253,9 @@ int k2w8_prepare_plain_i8(void *stream, const k2w8_prepare_plain_cfg *cfg, int64
   return ok();
 }
 
-// Fused prepare -> gemm_i8: validate both halves as their own entry points do, run the
-// one-launch form where it exists for the shape, else the two launches.
-// A prepare (kind 0 norm, 1 plain, 2 gated) and the GEMM that reads its q / q_scale,
-// with the given epilogue. Both halves are validated before either launches.
+// One-call prepare -> GEMM: a prepare (kind 0 norm, 1 plain, 2 gated) and the GEMM that
+// reads its q / q_scale, with the given epilogue. Both halves are validated as their
+// own entry points validate them, before either launches.
 struct LinearPrepare {
   int kind;
   int64_t width, out_stride, gate_stride;
@@ -253,32 +274,17 @@ static int run_linear(const char *stage, const LinearPrepare &lp, int epi, void 
   if (gcfg->k_size != lp.width || gcfg->k_stride != lp.out_stride)
     return fail(K2W8_INVALID_ARGUMENT,
                 "%s: the GEMM's k_size and k_stride must be the prepare's width and out_stride", stage);
-  if (lp.kind == 0) {
-    if (!lp.norm_scale || !lp.mod_scale || !lp.mod_shift)
-      return fail(K2W8_INVALID_ARGUMENT, "%s: null norm or modulation vector", stage);
-    if (!aligned(lp.norm_scale, 16) || !aligned(lp.mod_scale, 16) || !aligned(lp.mod_shift, 16))
-      return fail(K2W8_INVALID_ARGUMENT, "%s: norm and modulation vectors must be 16-byte aligned", stage);
-    if (!(lp.eps >= 0.0f)) return fail(K2W8_INVALID_ARGUMENT, "%s: eps must be >= 0", stage);
-  }
-  if (lp.kind == 2) {
-    if (!lp.gate_in) return fail(K2W8_INVALID_ARGUMENT, "%s: null gate", stage);
-    if (lp.gate_stride < lp.width || lp.gate_stride > 65536 || lp.gate_stride % 8 != 0)
-      return fail(K2W8_INVALID_ARGUMENT, "%s: gate_stride must be a multiple of 8 in width..65536, got %lld",
-                  stage, (long long)lp.gate_stride);
-    if (!aligned(lp.gate_in, 16)) return fail(K2W8_INVALID_ARGUMENT, "%s: gate must be 16-byte aligned", stage);
-  }
+  if (lp.kind == 0 &&
+      (rc = check_norm_vectors(stage, lp.norm_scale, lp.mod_scale, lp.mod_shift, lp.eps)) != K2W8_OK)
+    return rc;
+  if (lp.kind == 2 && (rc = check_gate_input(stage, lp.gate_in, lp.width, lp.gate_stride)) != K2W8_OK)
+    return rc;
   if (epi == k2w8::kEpiResid && !gate) return fail(K2W8_INVALID_ARGUMENT, "%s: null residual gate", stage);
   if (gate && !aligned(gate, 16))
     return fail(K2W8_INVALID_ARGUMENT, "%s: the residual gate must be 16-byte aligned", stage);
   if ((rc = ensure_configured(stage)) != K2W8_OK) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (lp.kind == 2) {
-    hipError_t e = k2w8::prepare_gated_ready(s);
-    if (e == hipErrorStreamCaptureUnsupported)
-      return fail(K2W8_RUNTIME, "%s: the first gated call on a device must not be inside a stream capture "
-                  "(k2w8_prime_launches sets the device up beforehand)", stage);
-    if (e != hipSuccess) return runtime(stage, e);
-  }
+  if (lp.kind == 2 && (rc = gated_ready(stage, s)) != K2W8_OK) return rc;
   k2w8::PrepareLaunch p;
   p.h = lp.h;
   p.gate = lp.gate_in;
@@ -379,18 +385,9 @@ int k2w8_prepare_gated_i8(void *stream, const k2w8_prepare_gated_cfg *cfg, int64
   if (!cfg) return fail(K2W8_INVALID_ARGUMENT, "%s: null configuration", stage);
   int rc = check_prepare(stage, tokens, cfg->width, cfg->out_stride, attn, q, q_scale);
   if (rc != K2W8_OK) return rc;
-  if (!gate) return fail(K2W8_INVALID_ARGUMENT, "%s: null gate", stage);
-  if (cfg->gate_stride < cfg->width || cfg->gate_stride > 65536 || cfg->gate_stride % 8 != 0)
-    return fail(K2W8_INVALID_ARGUMENT,
-                "%s: gate_stride must be a multiple of 8 in width..65536, got %lld", stage,
-                (long long)cfg->gate_stride);
-  if (!aligned(gate, 16)) return fail(K2W8_INVALID_ARGUMENT, "%s: gate must be 16-byte aligned", stage);
+  if ((rc = check_gate_input(stage, gate, cfg->width, cfg->gate_stride)) != K2W8_OK) return rc;
   if ((rc = ensure_configured(stage)) != K2W8_OK) return rc;
-  hipError_t e = k2w8::prepare_gated_ready(static_cast<hipStream_t>(stream));
-  if (e == hipErrorStreamCaptureUnsupported)
-    return fail(K2W8_RUNTIME, "%s: the first call on a device must not be inside a stream capture "
-                "(k2w8_prime_launches sets the device up beforehand)", stage);
-  if (e != hipSuccess) return runtime(stage, e);
+  if ((rc = gated_ready(stage, static_cast<hipStream_t>(stream))) != K2W8_OK) return rc;
   k2w8::PrepareLaunch p;
   p.h = attn;
   p.gate = gate;
@@ -399,7 +396,7 @@ int k2w8_prepare_gated_i8(void *stream, const k2w8_prepare_gated_cfg *cfg, int64
   p.width = cfg->width;
   p.out_stride = cfg->out_stride;
   p.gate_stride = cfg->gate_stride;
-  e = k2w8::launch_prepare(2, static_cast<hipStream_t>(stream), tokens, p);
+  const hipError_t e = k2w8::launch_prepare(2, static_cast<hipStream_t>(stream), tokens, p);
   if (e != hipSuccess) return runtime(stage, e);
   return ok();
 }
