@@ -270,3 +270,62 @@ def test_config_validators_accept_the_reference_ranges_and_name_what_they_reject
         assert fn(ctypes.byref(cfg)) == L.K2W8_INVALID_ARGUMENT, fragment
         assert fragment in lib.k2w8_last_error().decode()
     assert lib.k2w8_validate_gemm_cfg(None) == L.K2W8_INVALID_ARGUMENT
+
+
+ODD = ctypes.c_void_p(0x10004)  # 4-byte aligned only
+
+
+@pytest.mark.parametrize("ptrs,eps,fragment", [
+    ((None, FAKE, FAKE), 1e-6, "null norm"),
+    ((FAKE, FAKE, None), 1e-6, "null norm"),
+    ((FAKE, ODD, FAKE), 1e-6, "aligned"),
+    ((FAKE, FAKE, FAKE), -1.0, "eps"),
+    ((FAKE, FAKE, FAKE), float("nan"), "eps"),
+])
+def test_norm_prepare_and_its_linear_reject_bad_norm_vectors(k2, ptrs, eps, fragment):
+    L = k2.lib()
+    norm = k2._lib.PrepareNormCfg(3072, 3072, eps)
+    gemm = k2._lib.GemmCfg(3072, 3072, 3072, 4, 0)
+    assert L.k2w8_prepare_norm_i8(None, ctypes.byref(norm), 4, FAKE, *ptrs, FAKE, FAKE) == -1
+    assert fragment in L.k2w8_last_error().decode()
+    for fn in (L.k2w8_linear_norm_i8, L.k2w8_linear_norm_swiglu_i8):
+        assert fn(None, ctypes.byref(norm), ctypes.byref(gemm), 4, FAKE, *ptrs, FAKE, FAKE, FAKE, FAKE,
+                  FAKE) == -1
+        assert fragment in L.k2w8_last_error().decode()
+
+
+def test_linear_entry_points_reject_what_either_half_rejects(k2):
+    L = k2.lib()
+    plain = k2._lib.PreparePlainCfg(3072, 3072)
+    gated = k2._lib.PrepareGatedCfg(3072, 3072, 15360)
+    gemm = k2._lib.GemmCfg(3072, 3072, 3072, 4, 0)
+    # the GEMM must read the prepare's output as written
+    other = k2._lib.GemmCfg(2048, 3072, 3072, 4, 0)
+    assert L.k2w8_linear_plain_i8(None, ctypes.byref(plain), ctypes.byref(other), 4, FAKE, FAKE, FAKE, FAKE,
+                                  FAKE, FAKE) == -1
+    assert "k_size" in L.k2w8_last_error().decode()
+    # a bad GEMM configuration, and a null GEMM configuration
+    bad = k2._lib.GemmCfg(3072, 3000, 3072, 4, 0)
+    assert L.k2w8_linear_plain_i8(None, ctypes.byref(plain), ctypes.byref(bad), 4, FAKE, FAKE, FAKE, FAKE,
+                                  FAKE, FAKE) == -1
+    assert "n_size" in L.k2w8_last_error().decode()
+    assert L.k2w8_linear_plain_i8(None, ctypes.byref(plain), None, 4, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE) == -1
+    assert "null configuration" in L.k2w8_last_error().decode()
+    # the gated prepare's gate: null, a short row stride, misaligned
+    for gate_in, stride, fragment in [(None, 15360, "null gate"), (FAKE, 2048, "gate_stride"),
+                                      (ODD, 15360, "aligned")]:
+        g = k2._lib.PrepareGatedCfg(3072, 3072, stride)
+        assert L.k2w8_linear_gated_resid_i8(None, ctypes.byref(g), ctypes.byref(gemm), 4, FAKE, gate_in, FAKE,
+                                            FAKE, FAKE, FAKE, FAKE, FAKE) == -1
+        assert fragment in L.k2w8_last_error().decode(), fragment
+    # the residual epilogue's per-channel gate
+    assert L.k2w8_linear_gated_resid_i8(None, ctypes.byref(gated), ctypes.byref(gemm), 4, FAKE, FAKE, FAKE,
+                                        FAKE, FAKE, FAKE, FAKE, None) == -1
+    assert "residual gate" in L.k2w8_last_error().decode()
+    assert L.k2w8_linear_plain_resid_i8(None, ctypes.byref(plain), ctypes.byref(gemm), 4, FAKE, FAKE, FAKE,
+                                        FAKE, FAKE, FAKE, None) == -1
+    assert "residual gate" in L.k2w8_last_error().decode()
+    # and the token count, as the prepares check it
+    assert L.k2w8_linear_plain_i8(None, ctypes.byref(plain), ctypes.byref(gemm), 0, FAKE, FAKE, FAKE, FAKE,
+                                  FAKE, FAKE) == -1
+    assert "tokens" in L.k2w8_last_error().decode()
