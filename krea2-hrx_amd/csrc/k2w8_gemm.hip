@@ -497,11 +497,6 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int bid, uint8_t *s
     for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
-#ifdef K2W8_AGPR_ACC
-  // An AGPR operand anywhere in the function makes the compiler select the MFMA form
-  // whose accumulator lives in AGPRs, keeping the accumulators out of the VGPR file.
-  asm volatile("; agpr hint %0" ::"a"(0));
-#endif
 
   const int kg = wave / kCw, cw = wave - kg * kCw;
   const int wm = cw / WN, wn = cw % WN;
@@ -718,65 +713,26 @@ inline GemmArgs args_of(const GemmLaunch &l, int epilogue) {
 }  // namespace gemm
 
 #ifndef K2W8_GEMM_NO_ENTRY
-// Wave grids of the 256-row tiles (waves along M x along N).
-#ifndef K2W8_BIG_WM
-#define K2W8_BIG_WM 4
-#endif
-#ifndef K2W8_MID_WM
-#define K2W8_MID_WM 4
-#endif
-#ifndef K2W8_BIG_WAVES
-#define K2W8_BIG_WAVES 8
-#endif
-constexpr int kBigWm = K2W8_BIG_WM, kBigWn = K2W8_BIG_WAVES / kBigWm;
-#ifndef K2W8_BIG_BK
-#define K2W8_BIG_BK 128
-#endif
-#ifndef K2W8_BIG_STAGES
-#define K2W8_BIG_STAGES 2
-#endif
-constexpr int kBigBk = K2W8_BIG_BK, kBigStages = K2W8_BIG_STAGES;
+// The 256-row tiles: eight waves, 4 (along M) x 2 (along N), 128-byte K steps, two
+// stages.
+constexpr int kBigWm = 4, kBigWn = 2, kBigBk = 128, kBigStages = 2;
 // A round of 128x128 tiles against a round of 256x256 ones (measured 27 us against
 // 61 us at K=3072), in units of tile width.
-#ifndef K2W8_TAIL_COST
-#define K2W8_TAIL_COST 115
-#endif
-constexpr int64_t kTailCost = K2W8_TAIL_COST;
-#ifndef K2W8_USE_192
-#define K2W8_USE_192 1
-#endif
-constexpr bool kUse192 = K2W8_USE_192;
-constexpr int kMidWm = K2W8_MID_WM, kMidWn = 8 / kMidWm;
+constexpr int64_t kTailCost = 115;
+constexpr int kMidWm = 4, kMidWn = 2;
 // Stages of the 64x64 tiles: four (64 KiB, two workgroups per CU) keep three K steps
 // in flight, which the short per-tile work of the mid-M shapes needs (QKV at M=256:
 // 16.1 -> 9.7 us). The 128x128 tiles keep two: more would cost them occupancy.
-#ifndef K2W8_S64_STAGES
-#define K2W8_S64_STAGES 4
-#endif
-#ifndef K2W8_S128_STAGES
-#define K2W8_S128_STAGES 2
-#endif
-constexpr int kS64Stages = K2W8_S64_STAGES, kS128Stages = K2W8_S128_STAGES;
+constexpr int kS64Stages = 4, kS128Stages = 2;
 // Split-K slices: 128x128 tiles of eight waves (2 x 4, each 64x32), whose lower four
 // waves issue the transfers, with three stages (one workgroup per CU, two K steps in
 // flight). Against four waves and two stages: M=256 down projection 19.8 -> 18.1 us,
 // M=512 26.4 -> 25.0 us. Deeper 64x64 pipelines (six or eight stages, one workgroup
 // per CU) were slower (QKV at M=256: 8.6 -> 9.1-9.4 us).
-#ifndef K2W8_SPLIT_WN
-#define K2W8_SPLIT_WN 4
-#endif
-#ifndef K2W8_SPLIT_STAGES
-#define K2W8_SPLIT_STAGES 3
-#endif
-constexpr int kSplitStages = K2W8_SPLIT_STAGES, kSplitWn = K2W8_SPLIT_WN;
-#ifndef K2W8_S64_KG
-#define K2W8_S64_KG 2
-#endif
-constexpr int kS64Kg = K2W8_S64_KG;
-#ifndef K2W8_T12864_STAGES
-#define K2W8_T12864_STAGES 3
-#endif
-constexpr int k12864Stages = K2W8_T12864_STAGES;
+constexpr int kSplitStages = 3, kSplitWn = 4;
+// The 64x64 tiles run as two K groups of four waves; the 128x64 tiles keep three
+// stages.
+constexpr int kS64Kg = 2, k12864Stages = 3;
 
 int device_cus() {
   static int cached[64];
@@ -792,14 +748,9 @@ int device_cus() {
 }
 
 // Token counts served by the few-token kernel (weights streamed, HBM-bound).
-#ifndef K2W8_SKINNY_MAX_TOKENS
-#define K2W8_SKINNY_MAX_TOKENS 32
-#endif
-constexpr int64_t kSkinnyMaxTokens = K2W8_SKINNY_MAX_TOKENS;
+constexpr int64_t kSkinnyMaxTokens = 32;
 // Fewest 128-byte K steps a split-K slice takes.
-#ifndef K2W8_SPLITK_MIN_STEPS
-#define K2W8_SPLITK_MIN_STEPS 4
-#endif
+constexpr int64_t kSplitMinSteps = 4;
 
 hipError_t launch_splitk_reduce(int epilogue, hipStream_t stream, const int32_t *parts, int splits,
                                 int64_t stride, const gemm::GemmArgs &g);
@@ -820,16 +771,16 @@ hipError_t configure_gemm_lds() {
 namespace {
 
 // Split K over 128x128 tiles when they would leave most CUs idle: enough slices to
-// give every CU a workgroup, each at least K2W8_SPLITK_MIN_STEPS K steps, within the
+// give every CU a workgroup, each at least kSplitMinSteps K steps, within the
 // workspace. Returns the K steps per slice, or 0 for no split.
 int splitk_steps(const GemmLaunch &l, int64_t cus, size_t workspace_bytes) {
   const int64_t tiles = ((l.m + 127) / 128) * (l.n / 128);
   const int64_t k_steps = l.k / 128;
-  if (tiles * 2 > cus || k_steps < 2 * K2W8_SPLITK_MIN_STEPS) return 0;
+  if (tiles * 2 > cus || k_steps < 2 * kSplitMinSteps) return 0;
   // As many splits as keep the grid to one workgroup per CU (one round): a second,
   // partial round costs more than the K steps it takes off each slice.
   int64_t splits = cus / tiles;
-  if (splits > k_steps / K2W8_SPLITK_MIN_STEPS) splits = k_steps / K2W8_SPLITK_MIN_STEPS;
+  if (splits > k_steps / kSplitMinSteps) splits = k_steps / kSplitMinSteps;
   const int64_t slice_bytes = l.m * l.n * 4;
   if (slice_bytes >= (int64_t)1 << 31) return 0;  // buffer offsets within a slice are 32-bit
   const int64_t fit = (int64_t)workspace_bytes / slice_bytes;
@@ -860,18 +811,16 @@ hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &l) {
   if (l.n % 256 == 0 && (tiles(256, 256) >= kCus || (tiles(256, 128) > kCus && 2 * tiles(256, 256) >= kCus))) {
     const int64_t tm = (l.m + 255) / 256, total = tm * (l.n / 256);
     cost256 = rounds(total) * 256;
-#ifndef K2W8_NO_TAIL_SPLIT
     const int64_t rest = total % kCus, nb = (total / kCus) * kCus / tm * 256;
     if (total >= kCus && rest > 0 && rest * 2 <= kCus && nb > 0 && nb < l.n &&
         ((l.m + 127) / 128) * ((l.n - nb) / 128) <= kCus) {
       n_big = nb;
       cost256 = (total / kCus) * 256 + kTailCost;
     }
-#endif
   }
   if (cost256 != INT64_MAX) {
     // 256x192 tiles read 11% more LDS bytes per MFMA: they must win by 5%.
-    if (kUse192 && l.n % 192 == 0 && 2 * tiles(256, 192) >= kCus &&
+    if (l.n % 192 == 0 && 2 * tiles(256, 192) >= kCus &&
         rounds(tiles(256, 192)) * 192 * 21 < cost256 * 20)
       return gemm::launch_tile<256, 192, 4, 2, 128, 2>(epilogue, stream, a);
     if (n_big == 0) return gemm::launch_tile<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>(epilogue, stream, a);
@@ -899,10 +848,8 @@ hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &l) {
   if (tiles(128, 128) >= kCus) return gemm::launch_tile<128, 128, 2, 2, 128, kS128Stages>(epilogue, stream, a);
   // 64x64 tiles read every operand byte 4x as often as 128x128 ones: past K=4096 the
   // split-K pass over 128x128 tiles moves fewer bytes.
-#ifndef K2W8_NO_12864
   if (tiles(128, 64) >= kCus && l.k <= 4096)
     return gemm::launch_tile<128, 64, 4, 2, 128, k12864Stages>(epilogue, stream, a);
-#endif
   if (tiles(64, 64) >= kCus && l.k <= 4096)
     return gemm::launch_tile<64, 64, 2, 2, 128, kS64Stages, kS64Kg>(epilogue, stream, a);
   const Workspace ws = l.workspace ? *l.workspace : splitk_workspace(stream);

@@ -31,16 +31,12 @@ struct GemmArgs {
   int64_t split_stride = 0;
 };
 
-#ifndef K2W8_SWZ_SHIFT
-#define K2W8_SWZ_SHIFT 1
-#endif
-
 // Staged operand rows are BK bytes = BK/16 chunks of 16 bytes. The chunk index is
 // XORed with bits of the row so that the consecutive rows one LDS cycle serves (one
 // chunk each) land on distinct banks.
 template <int BK>
 __device__ __forceinline__ int swz_key(int r) {
-  return (r >> K2W8_SWZ_SHIFT) & (BK / 16 - 1);
+  return (r >> 1) & (BK / 16 - 1);
 }
 
 // A pointer the compiler may hold in VGPRs, as the scalar-register operand the

@@ -547,20 +547,15 @@ __global__ __launch_bounds__(Bounds<T>::kThreads) void prepare_kernel(PrepareArg
 // row's compute (a round of one row per wave loads everything, then computes): with
 // cold rows, M=4544 20.6 -> 19.5 us, width 4096 24.6 -> 23.3 us. The gated prepare
 // loses a third at 8 (24.4 -> 35.0 us).
-#ifndef K2W8_PREPARE_WAVES_PER_CU
-#define K2W8_PREPARE_WAVES_PER_CU 32
-#endif
-#ifndef K2W8_PREPARE_NORM_WAVES_PER_CU
-#define K2W8_PREPARE_NORM_WAVES_PER_CU 8
-#endif
+constexpr int kPrepareWavesPerCu = 32, kNormWavesPerCu = 8;
 
 template <int kKind, int T, bool kSingle>
 hipError_t launch_team(hipStream_t stream, const PrepareArgs &a) {
   const int threads = 64 * a.wpt * a.teams;
   const int needed = (a.tokens + a.teams - 1) / a.teams;
-  const int waves = (kKind == kNorm && kSingle) ? K2W8_PREPARE_NORM_WAVES_PER_CU
+  const int waves = (kKind == kNorm && kSingle) ? kNormWavesPerCu
                     : kKind == kGated            ? kGatedWaves
-                                                 : K2W8_PREPARE_WAVES_PER_CU;
+                                                 : kPrepareWavesPerCu;
   int per_cu = waves / (a.wpt * a.teams);
   if (per_cu < 1) per_cu = 1;
   const int cap = device_cus() * per_cu;
@@ -572,9 +567,6 @@ hipError_t launch_team(hipStream_t stream, const PrepareArgs &a) {
   return hipGetLastError();
 }
 
-#ifndef K2W8_PREPARE_MAX_RUNS_PER_LANE
-#define K2W8_PREPARE_MAX_RUNS_PER_LANE 1
-#endif
 
 // Team shape for a row: the fewest waves (at most 16) that hold it with at most
 // `max_runs` runs of 16 elements per lane; single-wave teams are packed four to a
@@ -611,7 +603,7 @@ hipError_t launch_kind(hipStream_t stream, PrepareArgs a) {
   // wave (sum of squares from registers, factors in LDS); the plain prepare takes
   // three (fewer waves per row: 9728 wide 50.5 -> 41.8 us at M=4096); the gated one
   // one (more waves per row: its sigmoid makes each element dearer).
-  constexpr int kRuns = kKind == kNorm ? 4 : (kKind == kPlain ? 3 : K2W8_PREPARE_MAX_RUNS_PER_LANE);
+  constexpr int kRuns = kKind == kNorm ? 4 : (kKind == kPlain ? 3 : 1);
   int t = 1;
   team_shape(a, kRuns, kKind == kGated, t);
   if (a.wpt == 1) return launch_t<kKind, true>(t, stream, a);

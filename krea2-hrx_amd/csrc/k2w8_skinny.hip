@@ -332,18 +332,14 @@ hipError_t set_lds_stream() {
   return hipSuccess;
 }
 
-#ifndef K2W8_SK_LDS_KB
-#define K2W8_SK_LDS_KB 48
-#endif
-#ifndef K2W8_SK_PMAX
-#define K2W8_SK_PMAX 8
-#endif
+// LDS budget of a workgroup's rings (KiB), and the deepest ring.
+constexpr int kRingKb = 48, kRingMax = 8;
 
 // Ring depth: as many steps as fit the LDS budget per workgroup (at least 2).
 constexpr int ring_depth_of(int rb, int tb, int ar, int waves) {
   const int per_step = waves * (rb / 8 + tb * ar / 8);  // KiB
-  const int p = K2W8_SK_LDS_KB / per_step;
-  return p < 2 ? 2 : (p > K2W8_SK_PMAX ? K2W8_SK_PMAX : p);
+  const int p = kRingKb / per_step;
+  return p < 2 ? 2 : (p > kRingMax ? kRingMax : p);
 }
 
 // Workgroup shape: 16 rows, or for SwiGLU a whole gate|up group (32 rows) when 16
