@@ -1,0 +1,35 @@
+"""bench.py's contract on the CPU: it measures one GPU and says so for any other count,
+and its CPU baseline (the oracle on the host's cores) reports the fields the bench line
+carries, on a small budget."""
+
+import importlib.util
+import os
+import subprocess
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def load_bench():
+    spec = importlib.util.spec_from_file_location("bench", os.path.join(ROOT, "bench.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_more_than_one_gpu_is_refused_with_a_message():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_cpu_baseline_reports_its_sample_cores_and_single_thread_figure():
+    bench = load_bench()
+    out = bench.cpu_baseline(4096, 256, 256, 256, 0.2)
+    assert out["kind"] == "port" and out["unit"] == "TOPS" and out["value"] > 0
+    assert out["cores"] >= 1 and "tokens" in out["sample"]
+    single = out["single_thread"]
+    assert single["cores"] == 1 and single["value"] > 0
+    # the multi-threaded figure is not below the single-threaded one by much (same code)
+    assert out["value"] > 0.5 * single["value"]
