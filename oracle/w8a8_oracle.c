@@ -22,6 +22,14 @@
  *   epilogue_plain    exact KAT src/training/quantized.rs:220
  *   epilogue_resid    tests/quantized.rs:229-243 tolerance + closed form
  *   epilogue_swiglu   tests/quantized.rs:244-255 tolerance (exp unpinned, as above)
+ *   epilogue_bias     no reference counterpart (an extension); pinned by the arithmetic:
+ *                     a +-0 bias gives epilogue_plain bit for bit, a zero accumulator
+ *                     gives f16(bf16(bias)), and every output is within one bf16 ulp plus
+ *                     the f32 error bound of the f64 closed form acc*ws*as + bias
+ *   gemm_i8           the fused CPU GEMM (the timed baseline): equal to gemm_i32 followed
+ *                     by epilogue_plain, on one thread and on all
+ *   f16 / bf16        numpy binary16 and torch bfloat16 over random bit patterns and
+ *                     every class (zeros, subnormals, overflow boundary, infinities)
  *   rope_qknorm       tolerance test of tests/quantized.rs:85-166 against an f64 norm,
  *                     the f32 rotary sum and the exact v copy; the in-wave sum-of-squares
  *                     order and rsqrt are the Loom compiler's, so bit parity is unpinned
