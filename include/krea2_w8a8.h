@@ -549,6 +549,8 @@ int k2w8_validate_prepare_plain_cfg(const k2w8_prepare_plain_cfg *cfg);
 int k2w8_validate_prepare_gated_cfg(const k2w8_prepare_gated_cfg *cfg);
 
 /* Launch-shape rules of src/kernels/shape.rs:7-112. */
+/* The size arguments are the reference's usize values: for 0..2^40 the rules below
+ * answer as the reference does; outside that domain they return -1. */
 int64_t k2w8_shape_gemm_pitch(int64_t k);    /* shape.rs:105-107 */
 int64_t k2w8_shape_capacity(int64_t tokens); /* shape.rs:12-16 */
 int64_t k2w8_shape_gemm_grid_rows(int64_t tokens); /* shape.rs:110-112 */

@@ -700,17 +700,28 @@ int k2w8_validate_prepare_gated_cfg(const k2w8_prepare_gated_cfg *cfg) {
   return ok();
 }
 
-int64_t k2w8_shape_gemm_pitch(int64_t k) { return (k % 8192 == 0) ? k + 64 : k; }
+// The shape rules take the reference's usize sizes; here they answer for 0..2^40 and
+// return -1 outside it (a negative size, or one whose arithmetic would overflow).
+constexpr int64_t kShapeDomain = int64_t(1) << 40;
+
+int64_t k2w8_shape_gemm_pitch(int64_t k) {
+  if (k < 0 || k > kShapeDomain) return -1;
+  return (k % 8192 == 0) ? k + 64 : k;
+}
 
 // src/kernels/shape.rs:12-16
 int64_t k2w8_shape_capacity(int64_t tokens) {
+  if (tokens < 0 || tokens > kShapeDomain) return -1;
   int64_t tiles = (tokens + 16 + 31) / 32 * 32;
   int64_t blocks = (tokens + 63) / 64 * 64;
   return tiles > blocks ? tiles : blocks;
 }
 
 // src/kernels/shape.rs:110-112
-int64_t k2w8_shape_gemm_grid_rows(int64_t tokens) { return (tokens + 255) / 256; }
+int64_t k2w8_shape_gemm_grid_rows(int64_t tokens) {
+  if (tokens < 0 || tokens > kShapeDomain) return -1;
+  return (tokens + 255) / 256;
+}
 
 // src/kernels/shape.rs:97-99
 int k2w8_shape_gemm_schedule_rows(int64_t tokens) { return tokens >= 4096 ? 1 : 0; }

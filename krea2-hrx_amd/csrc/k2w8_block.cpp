@@ -28,6 +28,11 @@ int k2w8_prime_launches(void *stream);
 namespace {
 
 constexpr int kModRows = 6;  // prescale, preshift, pregate, postscale, postshift, postgate
+// Bounds of a block call's shape: the prepares' token limit and the widest operand any
+// of its GEMMs or prepares accepts; and of the block index (a row of the modulation
+// table).
+constexpr int64_t kMaxBlockTokens = int64_t(1) << 20, kMaxBlockWidth = 65536;
+constexpr int64_t kMaxBlockIndex = int64_t(1) << 20;
 
 int check_cfg(const k2w8_block_cfg *c, const char *stage) {
   char msg[256];
@@ -35,12 +40,15 @@ int check_cfg(const k2w8_block_cfg *c, const char *stage) {
     snprintf(msg, sizeof msg, "%s: null configuration", stage);
     return k2w8_fail_invalid(msg);
   }
-  if (c->tokens < 1 || c->hidden < 256 || c->inter < 256 || c->qkvg < c->hidden ||
-      c->gate_offset < 0 || c->gate_offset + c->hidden > c->qkvg) {
+  // Bounded first, so that the arithmetic below cannot overflow; the stage entry
+  // points then check each launch's own limits.
+  if (c->tokens < 1 || c->tokens > kMaxBlockTokens || c->hidden < 256 || c->hidden > kMaxBlockWidth ||
+      c->inter < 256 || c->inter > kMaxBlockWidth || c->qkvg < c->hidden || c->qkvg > kMaxBlockWidth ||
+      c->gate_offset < 0 || c->gate_offset > c->qkvg - c->hidden) {
     snprintf(msg, sizeof msg,
-             "%s: shape must have tokens >= 1, hidden and inter >= 256, and the gate half "
-             "(gate_offset + hidden) inside qkvg",
-             stage);
+             "%s: shape must have tokens in 1..%lld, hidden, inter and qkvg in 256..%lld, and the "
+             "gate half (gate_offset + hidden) inside qkvg",
+             stage, (long long)kMaxBlockTokens, (long long)kMaxBlockWidth);
     return k2w8_fail_invalid(msg);
   }
   return K2W8_OK;
@@ -182,8 +190,13 @@ int check_call(const k2w8_block_cfg *c, int64_t index, const k2w8_block_weights 
   int rc = check_cfg(c, stage);
   if (rc != K2W8_OK) return rc;
   char msg[256];
-  if (!w || !b || !b->mods || index < 0) {
+  if (!w || !b || !b->mods) {
     snprintf(msg, sizeof msg, "%s: null weights, buffers or modulation table", stage);
+    return k2w8_fail_invalid(msg);
+  }
+  if (index < 0 || index >= kMaxBlockIndex) {
+    snprintf(msg, sizeof msg, "%s: block index must be in 0..%lld, got %lld", stage,
+             (long long)(kMaxBlockIndex - 1), (long long)index);
     return k2w8_fail_invalid(msg);
   }
   return K2W8_OK;
@@ -289,7 +302,7 @@ int k2w8_blocks_record(void *stream, const k2w8_block_cfg *cfg, int64_t layers,
   const char *stage = "blocks_record";
   if (!out) return k2w8_fail_invalid("blocks_record: null output");
   *out = nullptr;
-  if (layers < 1) return k2w8_fail_invalid("blocks_record: layers must be >= 1");
+  if (layers < 1 || layers > kMaxBlockIndex) return k2w8_fail_invalid("blocks_record: layers must be in 1..2^20");
   for (int64_t i = 0; i < layers; ++i) {
     int rc = check_block(cfg, i, weights + i, buffers, stage);
     if (rc != K2W8_OK) return rc;
@@ -333,7 +346,7 @@ int k2w8_blocks_profile(void *stream, const k2w8_block_cfg *cfg, int64_t layers,
   const char *stage = "blocks_profile";
   if (!stage_us || stage_count < kStageCount)
     return k2w8_fail_invalid("blocks_profile: stage_us must hold k2w8_block_stage_count() values");
-  if (layers < 1) return k2w8_fail_invalid("blocks_profile: layers must be >= 1");
+  if (layers < 1 || layers > kMaxBlockIndex) return k2w8_fail_invalid("blocks_profile: layers must be in 1..2^20");
   for (int64_t i = 0; i < layers; ++i) {
     int rc = check_block(cfg, i, weights + i, buffers, stage);
     if (rc != K2W8_OK) return rc;
@@ -346,10 +359,14 @@ int k2w8_blocks_profile(void *stream, const k2w8_block_cfg *cfg, int64_t layers,
     if (!is_attn || attention) order.push_back(k);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  std::vector<hipEvent_t> ev(order.size() * (size_t)layers + 1);
+  std::vector<hipEvent_t> ev(order.size() * (size_t)layers + 1, nullptr);
   for (auto &x : ev) {
-    hipError_t e = hipEventCreate(&x);
-    if (e != hipSuccess) return k2w8_fail_runtime(stage, e);
+    const hipError_t e = hipEventCreate(&x);
+    if (e != hipSuccess) {
+      for (auto &y : ev)
+        if (y) (void)hipEventDestroy(y);
+      return k2w8_fail_runtime(stage, e);
+    }
   }
   int rc = K2W8_OK;
   size_t at = 0;

@@ -3,18 +3,20 @@
 // tests/test_abi_sanitized.py. The launchers are replaced by stubs that check their
 // preconditions: the shape limits, strides, 32-bit offset bounds, token ranges, pointer
 // presence and alignment each kernel relies on. The driver makes 400000 calls of the
-// GEMM, prepare and one-call linear entry points with edge values, random values and
-// mostly-valid configurations with one field off; every call the ABI accepts must meet
-// the preconditions, and none may trip a sanitizer.
+// GEMM, prepare and one-call linear entry points, and 100000 of the block entry points
+// (k2w8_block.cpp, which chain them with the attention step's), with edge values,
+// random values and mostly-valid configurations with one field off; every call the
+// ABI accepts must meet the preconditions, and none may trip a sanitizer.
 #include <hip/hip_runtime.h>
 #include <cstdio>
+#include <cstring>
 #include <cstdlib>
 #include <algorithm>
 #include <random>
 #include "krea2_w8a8.h"
 #include "k2w8_internal.hpp"
 
-static long g_gemm = 0, g_prep = 0, g_bad = 0;
+static long g_gemm = 0, g_prep = 0, g_other = 0, g_bad = 0;
 #define REQ(c) do { if (!(c)) { fprintf(stderr, "violated: %s (line %d)\n", #c, __LINE__); ++g_bad; } } while (0)
 static bool al(const void *p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
@@ -53,14 +55,41 @@ hipError_t launch_prepare_gemm(int, hipStream_t, int64_t, const PrepareLaunch &,
   return hipErrorNotSupported;
 }
 hipError_t launch_probe_mfma(hipStream_t, int64_t, int64_t, int, uint32_t, int32_t *) { return hipSuccess; }
-hipError_t launch_rope_qknorm(hipStream_t, const RopeLaunch &) { return hipSuccess; }
+hipError_t launch_rope_qknorm(hipStream_t, const RopeLaunch &l) {
+  ++g_other;
+  REQ(l.tokens >= 1 && l.tokens <= (1 << 20));
+  REQ(l.q_heads >= 1 && l.kv_heads >= 1 && (l.q_heads + 2 * l.kv_heads) * l.tokens < (1ll << 32));
+  REQ(l.row_stride % 8 == 0 && l.q_heads * 128 <= l.row_stride && l.k_offset % 8 == 0 &&
+      l.k_offset + 2 * l.kv_heads * 128 <= l.row_stride);
+  REQ(l.qkv && l.q_scale && l.k_scale && l.cos && l.sin && l.q_out && l.k_out && l.v_out);
+  REQ(al(l.qkv, 16) && al(l.q_out, 16) && al(l.k_out, 16) && al(l.v_out, 16) && al(l.cos, 16) && al(l.sin, 16));
+  return hipSuccess;
+}
 hipError_t launch_sigmoid(hipStream_t, int64_t, const float *, float *) { return hipSuccess; }
 hipError_t launch_transport(int, hipStream_t, int64_t, const void *, void *) { return hipSuccess; }
-hipError_t launch_v_transpose(hipStream_t, int64_t, int64_t, int64_t, const void *, void *) { return hipSuccess; }
-hipError_t launch_attention(hipStream_t, const AttentionLaunch &) { return hipSuccess; }
+hipError_t launch_v_transpose(hipStream_t, int64_t rows, int64_t width, int64_t capacity, const void *x,
+                              void *out) {
+  ++g_other;
+  REQ(rows >= 1 && rows <= capacity && capacity % 8 == 0 && width % 8 == 0 && width >= 8);
+  REQ(width * capacity < (1ll << 40) && x && out && al(x, 16) && al(out, 16));
+  return hipSuccess;
+}
+hipError_t launch_attention(hipStream_t, const AttentionLaunch &l) {
+  ++g_other;
+  REQ(l.group == 1 || l.group == 2 || l.group == 4);
+  REQ(l.tokens >= 16 && l.capacity >= l.tokens + 16 && l.capacity % 16 == 0 && l.capacity <= (1 << 20));
+  REQ(l.rows_out >= 1 && l.rows_out <= l.tokens);
+  REQ(l.q_stride % 128 == 0 && l.kv_stride % 128 == 0 && l.out_stride % 128 == 0);
+  REQ(l.kv_heads >= 1 && l.kv_heads * 128 <= l.kv_stride && l.group * l.kv_heads * 128 <= l.q_stride &&
+      l.group * l.kv_heads * 128 <= l.out_stride);
+  REQ(l.scale > 0.0f && l.q && l.k && l.vt && l.out && al(l.q, 16) && al(l.k, 16) && al(l.vt, 16) &&
+      al(l.out, 16));
+  return hipSuccess;
+}
 hipError_t splitk_register(hipStream_t, void *, size_t) { return hipSuccess; }
 size_t splitk_workspace_bytes() { return 64u << 20; }
 Workspace splitk_static_scratch(hipError_t *e) { *e = hipSuccess; return Workspace{(void *)0x100000, 16u << 20}; }
+void splitk_install(Workspace) {}
 }  // namespace k2w8
 
 int main() {
@@ -127,6 +156,46 @@ int main() {
       }
     }
   }
-  printf("gemm launches %ld, prepare launches %ld, violations %ld\n", g_gemm, g_prep, g_bad);
+  // The block entry points (k2w8_block.cpp), which chain the stage calls above and
+  // the attention step's, over edge, huge and mostly-valid block shapes and indices.
+  const int64_t bedge[] = {-1, 0, 1, 15, 16, 128, 255, 256, 384, 512, 1024, 3072, 6144, 9216, 12288, 15360,
+                           16384, 1 << 20, 1ll << 31, 1ll << 40, INT64_MAX - 5, INT64_MAX, INT64_MIN};
+  auto bpick = [&]() -> int64_t { return bedge[rng() % (sizeof bedge / 8)]; };
+  long blocks_accepted = 0;
+  for (int it = 0; it < 100000; ++it) {
+    k2w8_block_cfg c{bpick(), bpick(), bpick(), bpick(), bpick(), 1e-5f};
+    if (rng() % 2) {
+      c.tokens = 1 + (int64_t)(rng() % 5000);
+      c.hidden = 256 * (1 + (int64_t)(rng() % 24));
+      c.inter = 256 * (1 + (int64_t)(rng() % 64));
+      c.gate_offset = c.hidden + 256 * (int64_t)(rng() % 8);
+      c.qkvg = c.gate_offset + c.hidden + (int64_t)(rng() % 3) * 128;
+    }
+    k2w8_block_weights w;
+    memset(&w, 0, sizeof w);
+    const void **wp = reinterpret_cast<const void **>(&w);
+    for (size_t i = 0; i < sizeof w / sizeof(void *); ++i) wp[i] = rng() % 10 ? (void *)0x10000 : nullptr;
+    k2w8_block_buffers b;
+    memset(&b, 0, sizeof b);
+    void **bp = reinterpret_cast<void **>(&b);
+    for (size_t i = 0; i < sizeof b / sizeof(void *); ++i) bp[i] = rng() % 10 ? (void *)0x10000 : nullptr;
+    const int64_t index = rng() % 4 ? (int64_t)(rng() % 64) : bpick();
+    int rc;
+    switch (rng() % 3) {
+      case 0: rc = k2w8_block_pre_attention(nullptr, &c, index, &w, &b); break;
+      case 1: rc = k2w8_block_attention(nullptr, &c, index, &w, &b); break;
+      default: rc = k2w8_block_post_attention(nullptr, &c, index, &w, &b); break;
+    }
+    blocks_accepted += rc == K2W8_OK;
+  }
+  // The shape rules outside their domain.
+  for (int64_t v : bedge) {
+    (void)k2w8_shape_gemm_pitch(v);
+    (void)k2w8_shape_capacity(v);
+    (void)k2w8_shape_gemm_grid_rows(v);
+    (void)k2w8_shape_gemm_schedule_rows(v);
+  }
+  printf("gemm launches %ld, prepare launches %ld, other launches %ld, blocks accepted %ld, violations %ld\n",
+         g_gemm, g_prep, g_other, blocks_accepted, g_bad);
   return g_bad ? 1 : 0;
 }

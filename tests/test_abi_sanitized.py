@@ -1,5 +1,5 @@
 """The C ABI's validation on the CPU, under AddressSanitizer and UndefinedBehaviorSanitizer:
-every GEMM, prepare and one-call linear entry point is driven with edge and random
+every GEMM, prepare, one-call linear and block entry point is driven with edge and random
 arguments (tests/fuzz/abi_validation.cpp), with the kernel launchers replaced by stubs
 that check the preconditions the kernels rely on. Accepted calls must meet them all;
 rejected ones must return an error code, with no sanitizer report either way."""
@@ -23,6 +23,7 @@ def test_accepted_calls_meet_the_launchers_preconditions(tmp_path):
            "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", f"-I{ROOT}/include",
            f"-I{ROOT}/krea2-hrx_amd/csrc", os.path.join(HERE, "fuzz", "abi_validation.cpp"),
            os.path.join(ROOT, "krea2-hrx_amd", "csrc", "k2w8_api.cpp"),
+           os.path.join(ROOT, "krea2-hrx_amd", "csrc", "k2w8_block.cpp"),
            f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-o", str(exe)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0 and "sanitize" in r.stderr:
@@ -33,4 +34,5 @@ def test_accepted_calls_meet_the_launchers_preconditions(tmp_path):
     assert r.returncode == 0, (r.stdout + r.stderr)[-4000:]
     counts = dict(part.rsplit(" ", 1) for part in r.stdout.strip().split(", "))
     assert int(counts["gemm launches"]) > 1000 and int(counts["prepare launches"]) > 1000
+    assert int(counts["other launches"]) > 100 and int(counts["blocks accepted"]) > 1000
     assert counts["violations"] == "0"
