@@ -194,12 +194,32 @@ int64_t k2w8_gemm_workspace_bytes(void);
  * partial sums go to a 16 MiB static device array of the library (one per device,
  * held until the process ends) instead of any workspace, so no call allocates
  * device memory. A shape that would split K into slices of which two do not fit
- * (2 * m * n_size * 4 bytes > 16 MiB) is refused with INVALID_ARGUMENT; the split
- * rule of this build never picks one. Every call on a device shares that device's
+ * (2 * m * n_size * 4 bytes > 16 MiB) is refused with INVALID_ARGUMENT; on a 256-CU
+ * MI355X the split rule never picks one (it splits only when the 128x128 tiles cover
+ * at most half the CUs, so m * n_size <= 2^21). Every call on a device shares that device's
  * array: calls that overlap on one device (on different streams) race on it.
  */
 int k2w8_gemm_i8_noalloc(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, const int8_t *a,
                          const int8_t *w, const float *scale, const float *a_scale, void *c);
+
+/*
+ * gemm_choose: no counterpart in the reference. Which kernel the GEMM entry points run
+ * for a shape on a device with `cus` compute units and a split-K workspace of
+ * `workspace_bytes` (the library's own: k2w8_gemm_workspace_bytes()), without launching
+ * anything: the rule launch_gemm applies, for tuning reports and host-side tests.
+ * `epilogue` is 0 plain, 1 residual, 2 SwiGLU, 3 bias, 4 int32 accumulators.
+ */
+typedef struct k2w8_gemm_choice {
+  int32_t kernel;  /* 0 few-token kernel, 1 tile kernel, 2 256x256 tiles then the last
+                      columns as 128x128 tiles, 3 split K over 128x128 tiles + reduction */
+  int32_t tile_m, tile_n; /* kernels 1-3: the workgroup tile (kernel 2: 256x256) */
+  int32_t stages;         /* kernels 1-3: LDS stages of the tile kernel */
+  int64_t n_big;          /* kernel 2: the columns that run as 256x256 tiles */
+  int32_t split_steps;    /* kernel 3: 128-byte K steps per slice */
+  int32_t splits;         /* kernel 3: slices */
+} k2w8_gemm_choice;
+int k2w8_gemm_choose(int32_t epilogue, int64_t m, const k2w8_gemm_cfg *cfg, int64_t cus,
+                     int64_t workspace_bytes, k2w8_gemm_choice *out);
 
 /*
  * linear_norm_i8 / linear_plain_i8: one call for a projection:

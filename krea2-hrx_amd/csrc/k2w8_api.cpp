@@ -11,6 +11,7 @@
 
 #include "krea2_w8a8.h"
 #include "k2w8_internal.hpp"
+#include "k2w8_gemm_plan.hpp"
 
 namespace {
 
@@ -444,6 +445,51 @@ int k2w8_gemm_i8_noalloc(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, cons
   if (e != hipSuccess) return runtime("gemm_i8_noalloc: the static scratch's device address", e);
   return run_gemm(stage, k2w8::kEpiPlain, stream, cfg, m, a, w, scale, a_scale, c, nullptr,
                   nullptr, &scratch);
+}
+
+int k2w8_gemm_choose(int32_t epilogue, int64_t m, const k2w8_gemm_cfg *cfg, int64_t cus,
+                     int64_t workspace_bytes, k2w8_gemm_choice *out) {
+  const char *stage = "gemm_choose";
+  if (!cfg || !out) return fail(K2W8_INVALID_ARGUMENT, "%s: null configuration or output", stage);
+  int rc = check_gemm_cfg(stage, cfg);
+  if (rc != K2W8_OK) return rc;
+  if (epilogue < 0 || epilogue > k2w8::kEpiAcc)
+    return fail(K2W8_INVALID_ARGUMENT, "%s: epilogue must be 0..4, got %d", stage, (int)epilogue);
+  if (m < 1 || m > 16777216)
+    return fail(K2W8_INVALID_ARGUMENT, "%s: m must be 1..16777216, got %lld", stage, (long long)m);
+  if (cus < 1 || cus > 4096 || workspace_bytes < 0)
+    return fail(K2W8_INVALID_ARGUMENT, "%s: cus must be 1..4096 and workspace_bytes >= 0", stage);
+  k2w8::GemmLaunch l;
+  l.m = m;
+  l.n = cfg->n_size;
+  l.k = cfg->k_size;
+  l.lda = cfg->k_stride;
+  *out = k2w8_gemm_choice{};
+  if (k2w8::gemm_streams(epilogue, l, cus)) return ok();  // kernel 0
+  using k2w8::GemmTile;
+  const k2w8::TilePlan plan = k2w8::plan_tiles(l.m, l.n, l.k, cus);
+  struct Shape {
+    int32_t m, n, stages;
+  };
+  static const Shape kShapes[] = {{256, 256, 2}, {256, 192, 2}, {256, 128, 2}, {256, 128, 3},
+                                  {128, 128, 2}, {128, 64, 3},  {64, 64, 4},   {128, 128, 3}};
+  int tile = (int)plan.tile;
+  out->kernel = plan.n_big > 0 ? 2 : 1;
+  out->n_big = plan.n_big;
+  if (plan.tile == GemmTile::kSplit) {
+    const int per = k2w8::splitk_steps(l.m, l.n, l.k, cus, (size_t)workspace_bytes);
+    if (per > 0) {
+      out->kernel = 3;
+      out->split_steps = per;
+      out->splits = (int32_t)((l.k / 128 + per - 1) / per);
+    } else {
+      tile = (int)GemmTile::k64x64;  // no split without room for two slices
+    }
+  }
+  out->tile_m = kShapes[tile].m;
+  out->tile_n = kShapes[tile].n;
+  out->stages = kShapes[tile].stages;
+  return ok();
 }
 
 int k2w8_gemm_set_workspace(void *stream, void *workspace, int64_t bytes) {

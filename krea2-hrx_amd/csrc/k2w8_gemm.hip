@@ -18,6 +18,7 @@
 #include <stdint.h>
 
 #include "k2w8_gemm_common.hpp"
+#include "k2w8_gemm_plan.hpp"
 #include "k2w8_internal.hpp"
 #include "k2w8_numerics.hpp"
 
@@ -716,9 +717,6 @@ inline GemmArgs args_of(const GemmLaunch &l, int epilogue) {
 // The 256-row tiles: eight waves, 4 (along M) x 2 (along N), 128-byte K steps, two
 // stages.
 constexpr int kBigWm = 4, kBigWn = 2, kBigBk = 128, kBigStages = 2;
-// A round of 128x128 tiles against a round of 256x256 ones (measured 27 us against
-// 61 us at K=3072), in units of tile width.
-constexpr int64_t kTailCost = 115;
 constexpr int kMidWm = 4, kMidWn = 2;
 // Stages of the 64x64 tiles: four (64 KiB, two workgroups per CU) keep three K steps
 // in flight, which the short per-tile work of the mid-M shapes needs (QKV at M=256:
@@ -749,8 +747,6 @@ int device_cus() {
 
 // Token counts served by the few-token kernel (weights streamed, HBM-bound).
 constexpr int64_t kSkinnyMaxTokens = 32;
-// Fewest 128-byte K steps a split-K slice takes.
-constexpr int64_t kSplitMinSteps = 4;
 
 hipError_t launch_splitk_reduce(int epilogue, hipStream_t stream, const int32_t *parts, int splits,
                                 int64_t stride, const gemm::GemmArgs &g);
@@ -768,110 +764,66 @@ hipError_t configure_gemm_lds() {
   return e;
 }
 
-namespace {
-
-// Split K over 128x128 tiles when they would leave most CUs idle: enough slices to
-// give every CU a workgroup, each at least kSplitMinSteps K steps, within the
-// workspace. Returns the K steps per slice, or 0 for no split.
-int splitk_steps(const GemmLaunch &l, int64_t cus, size_t workspace_bytes) {
-  const int64_t tiles = ((l.m + 127) / 128) * (l.n / 128);
-  const int64_t k_steps = l.k / 128;
-  if (tiles * 2 > cus || k_steps < 2 * kSplitMinSteps) return 0;
-  // As many splits as keep the grid to one workgroup per CU (one round): a second,
-  // partial round costs more than the K steps it takes off each slice.
-  int64_t splits = cus / tiles;
-  if (splits > k_steps / kSplitMinSteps) splits = k_steps / kSplitMinSteps;
-  const int64_t slice_bytes = l.m * l.n * 4;
-  if (slice_bytes >= (int64_t)1 << 31) return 0;  // buffer offsets within a slice are 32-bit
-  const int64_t fit = (int64_t)workspace_bytes / slice_bytes;
-  if (splits > fit) splits = fit;
-  if (splits < 2) return 0;
-  const int64_t per = (k_steps + splits - 1) / splits;
-  return (k_steps + per - 1) / per >= 2 ? (int)per : 0;
+bool gemm_streams(int epilogue, const GemmLaunch &l, int64_t cus) {
+  return l.m <= kSkinnyMaxTokens || skinny_streams(epilogue, l, cus);
 }
 
-}  // namespace
-
-// Tile choice: 256x256 or 256x192 when they give at least a full round (or, for one
-// round, half the CUs), by rounds x width; else 256x128 when it gives every CU a
-// workgroup (three stages when it gives more than half of them one, for M > 128);
-// 128x128 when it gives every CU a workgroup; 64x64 for K up to 4096; split K over
-// 128x128 tiles when those cover at most half the CUs; else 64x64.
+// The few-token kernel, or the tile kernel plan_tiles picks (k2w8_gemm_plan.hpp).
 hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &l) {
-  if (l.m <= kSkinnyMaxTokens || skinny_streams(epilogue, l)) return launch_skinny(epilogue, stream, l);
+  const int64_t cus = device_cus();
+  if (gemm_streams(epilogue, l, cus)) return launch_skinny(epilogue, stream, l);
   gemm::GemmArgs a = gemm::args_of(l, epilogue);
-  auto tiles = [&](int64_t bm, int64_t bn) { return ((l.m + bm - 1) / bm) * (l.n / bn); };
-  const int64_t kCus = device_cus();
-  // Wide tiles. A tile's time is about proportional to its width, so the candidates
-  // compare by rounds x width: 256x256 (whole rounds, the columns of a last, mostly
-  // idle round re-tiled as one round of 128x128 tiles, about 0.45 of a 256x256 round),
-  // or 256x192. Measured: QKV 4096x9216 144 -> 135 us, config 1 (4096x3072) 52 -> 46 us.
-  auto rounds = [&](int64_t t) { return (t + kCus - 1) / kCus; };
-  int64_t cost256 = INT64_MAX, n_big = 0;
-  if (l.n % 256 == 0 && (tiles(256, 256) >= kCus || (tiles(256, 128) > kCus && 2 * tiles(256, 256) >= kCus))) {
-    const int64_t tm = (l.m + 255) / 256, total = tm * (l.n / 256);
-    cost256 = rounds(total) * 256;
-    const int64_t rest = total % kCus, nb = (total / kCus) * kCus / tm * 256;
-    if (total >= kCus && rest > 0 && rest * 2 <= kCus && nb > 0 && nb < l.n &&
-        ((l.m + 127) / 128) * ((l.n - nb) / 128) <= kCus) {
-      n_big = nb;
-      cost256 = (total / kCus) * 256 + kTailCost;
-    }
-  }
-  if (cost256 != INT64_MAX) {
-    // 256x192 tiles read 11% more LDS bytes per MFMA: they must win by 5%.
-    if (l.n % 192 == 0 && 2 * tiles(256, 192) >= kCus &&
-        rounds(tiles(256, 192)) * 192 * 21 < cost256 * 20)
+  const TilePlan plan = plan_tiles(l.m, l.n, l.k, cus);
+  switch (plan.tile) {
+    case GemmTile::k256x192:
       return gemm::launch_tile<256, 192, 4, 2, 128, 2>(epilogue, stream, a);
-    if (n_big == 0) return gemm::launch_tile<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>(epilogue, stream, a);
-    gemm::GemmArgs big = a, tail = a;
-    big.n = (int)n_big;
-    hipError_t e = gemm::launch_tile<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>(epilogue, stream, big);
-    if (e != hipSuccess) return e;
-    tail.n = (int)(l.n - n_big);
-    tail.w = a.w + n_big * l.lda;
-    tail.w_scale = a.w_scale + n_big;
-    if (tail.gate) tail.gate = a.gate + n_big;
-    if (tail.bias) tail.bias = a.bias + n_big;
-    const int64_t out_col = epilogue == kEpiSwiglu ? n_big / 2 : n_big;
-    const int64_t elem = epilogue == kEpiAcc ? 4 : 2;
-    tail.c = static_cast<char *>(a.c) + out_col * elem;
-    return gemm::launch_tile<128, 128, 2, 2, 128, kS128Stages>(epilogue, stream, tail);
+    case GemmTile::k256x256: {
+      if (plan.n_big == 0) return gemm::launch_tile<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>(epilogue, stream, a);
+      gemm::GemmArgs big = a, tail = a;
+      big.n = (int)plan.n_big;
+      hipError_t e = gemm::launch_tile<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>(epilogue, stream, big);
+      if (e != hipSuccess) return e;
+      tail.n = (int)(l.n - plan.n_big);
+      tail.w = a.w + plan.n_big * l.lda;
+      tail.w_scale = a.w_scale + plan.n_big;
+      if (tail.gate) tail.gate = a.gate + plan.n_big;
+      if (tail.bias) tail.bias = a.bias + plan.n_big;
+      const int64_t out_col = epilogue == kEpiSwiglu ? plan.n_big / 2 : plan.n_big;
+      const int64_t elem = epilogue == kEpiAcc ? 4 : 2;
+      tail.c = static_cast<char *>(a.c) + out_col * elem;
+      return gemm::launch_tile<128, 128, 2, 2, 128, kS128Stages>(epilogue, stream, tail);
+    }
+    case GemmTile::k256x128:
+      return gemm::launch_tile<256, 128, kMidWm, kMidWn, 128, 2>(epilogue, stream, a);
+    case GemmTile::k256x128Deep:
+      return gemm::launch_tile<256, 128, kMidWm, kMidWn, 128, 3>(epilogue, stream, a);
+    case GemmTile::k128x128:
+      return gemm::launch_tile<128, 128, 2, 2, 128, kS128Stages>(epilogue, stream, a);
+    case GemmTile::k128x64:
+      return gemm::launch_tile<128, 64, 4, 2, 128, k12864Stages>(epilogue, stream, a);
+    case GemmTile::k64x64:
+      return gemm::launch_tile<64, 64, 2, 2, 128, kS64Stages, kS64Kg>(epilogue, stream, a);
+    case GemmTile::kSplit:
+      break;
   }
-  if (tiles(256, 128) >= kCus)
-    return gemm::launch_tile<256, 128, kMidWm, kMidWn, 128, 2>(epilogue, stream, a);
-  // One round of 256x128 tiles over more than half the CUs: one workgroup per CU, so
-  // three stages fit (two K steps in flight). SwiGLU-up at M=256: 34.6 -> 31.3 us
-  // against 128x128 tiles.
-  if (l.m > 128 && 2 * tiles(256, 128) > kCus)
-    return gemm::launch_tile<256, 128, kMidWm, kMidWn, 128, 3>(epilogue, stream, a);
-  if (tiles(128, 128) >= kCus) return gemm::launch_tile<128, 128, 2, 2, 128, kS128Stages>(epilogue, stream, a);
-  // 64x64 tiles read every operand byte 4x as often as 128x128 ones: past K=4096 the
-  // split-K pass over 128x128 tiles moves fewer bytes.
-  if (tiles(128, 64) >= kCus && l.k <= 4096)
-    return gemm::launch_tile<128, 64, 4, 2, 128, k12864Stages>(epilogue, stream, a);
-  if (tiles(64, 64) >= kCus && l.k <= 4096)
-    return gemm::launch_tile<64, 64, 2, 2, 128, kS64Stages, kS64Kg>(epilogue, stream, a);
   const Workspace ws = l.workspace ? *l.workspace : splitk_workspace(stream);
   // A caller that passes a fixed workspace and requires it: a shape that would split K
   // but whose two slices do not fit is refused before anything is launched.
-  if (l.workspace_required && splitk_steps(l, kCus, SIZE_MAX) > 0 &&
+  if (l.workspace_required && splitk_steps(l.m, l.n, l.k, cus, SIZE_MAX) > 0 &&
       (size_t)(2 * l.m * l.n * 4) > ws.bytes)
     return hipErrorInvalidValue;
-  const int per = ws.ptr ? splitk_steps(l, kCus, ws.bytes) : 0;
+  const int per = ws.ptr ? splitk_steps(l.m, l.n, l.k, cus, ws.bytes) : 0;
   if (per > 0) {
     int32_t *parts = static_cast<int32_t *>(ws.ptr);
-    {
-      const int splits = (int)((l.k / 128 + per - 1) / per);
-      gemm::GemmArgs p = a;
-      p.c = parts;
-      p.ldc = (int)l.n;
-      p.k_split_steps = per;
-      p.split_stride = l.m * l.n;
-      hipError_t e = gemm::launch_tile<128, 128, 2, kSplitWn, 128, kSplitStages>(kEpiAcc, stream, p);
-      if (e != hipSuccess) return e;
-      return launch_splitk_reduce(epilogue, stream, parts, splits, l.m * l.n, a);
-    }
+    const int splits = (int)((l.k / 128 + per - 1) / per);
+    gemm::GemmArgs p = a;
+    p.c = parts;
+    p.ldc = (int)l.n;
+    p.k_split_steps = per;
+    p.split_stride = l.m * l.n;
+    hipError_t e = gemm::launch_tile<128, 128, 2, kSplitWn, 128, kSplitStages>(kEpiAcc, stream, p);
+    if (e != hipSuccess) return e;
+    return launch_splitk_reduce(epilogue, stream, parts, splits, l.m * l.n, a);
   }
   return gemm::launch_tile<64, 64, 2, 2, 128, kS64Stages, kS64Kg>(epilogue, stream, a);
 }

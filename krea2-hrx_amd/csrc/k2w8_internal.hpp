@@ -54,7 +54,9 @@ hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &g);
 hipError_t launch_prepare_gemm(int kind, hipStream_t stream, int64_t tokens, const PrepareLaunch &p,
                                const GemmLaunch &g);
 // Few-token kernel (any m; chosen by launch_gemm for small m).
-bool skinny_streams(int epilogue, const GemmLaunch &g);
+bool skinny_streams(int epilogue, const GemmLaunch &g, int64_t cus);
+// The few-token kernel's choice (M <= 32, or skinny_streams) with `cus` CUs.
+bool gemm_streams(int epilogue, const GemmLaunch &g, int64_t cus);
 hipError_t launch_skinny(int epilogue, hipStream_t stream, const GemmLaunch &g);
 hipError_t configure_gemm_lds();
 hipError_t configure_skinny_lds();

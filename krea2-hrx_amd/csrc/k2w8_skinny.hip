@@ -353,7 +353,7 @@ constexpr int ring_depth_of(int rb, int tb, int ar, int waves) {
 // and twice the workgroups cost more than they even out (M=16 12.3 -> 12.7, M=32 14.0
 // -> 16.2), so there the workgroups keep whole groups.
 int rows_of(int epi, int ar) { return epi == kEpiSwiglu && ar == 16 ? 32 : 16; }
-int waves_of(int epi, int64_t n) { return epi != kEpiSwiglu && n / 16 < device_cus() ? 8 : 4; }
+int waves_of(int epi, int64_t n, int64_t cus) { return epi != kEpiSwiglu && n / 16 < cus ? 8 : 4; }
 
 template <int RB, int TB, int AR, int WAVES>
 hipError_t launch_rows(int epi, hipStream_t stream, const Args &a) {
@@ -364,7 +364,7 @@ template <int TB, int AR>
 hipError_t launch_tb(int epi, hipStream_t stream, const Args &a) {
   if constexpr (AR == 16)
     if (epi == kEpiSwiglu) return launch_rows<32, TB, AR, 4>(epi, stream, a);
-  if (waves_of(epi, a.n) == 8) return launch_rows<16, TB, AR, 8>(epi, stream, a);
+  if (waves_of(epi, a.n, device_cus()) == 8) return launch_rows<16, TB, AR, 8>(epi, stream, a);
   return launch_rows<16, TB, AR, 4>(epi, stream, a);
 }
 
@@ -383,15 +383,15 @@ hipError_t set_lds_tb() {
 // grid (one workgroup per RB weight rows and per 64 tokens) is resident at once:
 // measured at K=2560, N=4096, M=64-128: 12-15 -> 7-9 us; where the grid takes two
 // rounds (N=19456, M=64) or K is long (9728), the tile kernels are faster.
-bool skinny_streams(int epilogue, const GemmLaunch &l) {
+bool skinny_streams(int epilogue, const GemmLaunch &l, int64_t cus) {
   if (l.m > 128 || l.k > 4096) return false;
   const int64_t tokens = l.m < skinny::kTokensPerGroup ? l.m : skinny::kTokensPerGroup;
   const int tb = (int)((tokens + 15) / 16), ar = tokens <= 8 ? 8 : 16;
-  const int rb = skinny::rows_of(epilogue, ar), waves = skinny::waves_of(epilogue, l.n);
+  const int rb = skinny::rows_of(epilogue, ar), waves = skinny::waves_of(epilogue, l.n, cus);
   const int lds_kb = waves * skinny::ring_depth_of(rb, tb, ar, waves) * (rb / 8 + tb * ar / 8);
   const int64_t per_cu = 160 / lds_kb;
   const int64_t grid = (l.n / rb) * ((l.m + skinny::kTokensPerGroup - 1) / skinny::kTokensPerGroup);
-  return grid <= per_cu * device_cus();
+  return grid <= per_cu * cus;
 }
 
 hipError_t configure_skinny_lds() {

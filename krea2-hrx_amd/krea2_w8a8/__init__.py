@@ -24,6 +24,7 @@ from .ops import (  # noqa: F401
     gemm_i8_resid,
     gemm_i8_resid_256x256,
     gemm_i8_swiglu,
+    gemm_choose,
     gemm_set_workspace,
     gemm_workspace_bytes,
     linear_gated_resid_i8,
@@ -55,6 +56,7 @@ __all__ = [
     "gemm_i8_resid",
     "gemm_i8_resid_256x256",
     "gemm_i8_swiglu",
+    "gemm_choose",
     "gemm_set_workspace",
     "gemm_workspace_bytes",
     "lib",

@@ -121,6 +121,18 @@ class GemmCfg(ctypes.Structure):
     ]
 
 
+class GemmChoice(ctypes.Structure):
+    _fields_ = [
+        ("kernel", ctypes.c_int32),
+        ("tile_m", ctypes.c_int32),
+        ("tile_n", ctypes.c_int32),
+        ("stages", ctypes.c_int32),
+        ("n_big", ctypes.c_int64),
+        ("split_steps", ctypes.c_int32),
+        ("splits", ctypes.c_int32),
+    ]
+
+
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 
@@ -147,6 +159,8 @@ SIGNATURES = {
     "k2w8_gemm_i8_bias": (ctypes.c_int, [_P, ctypes.POINTER(GemmCfg), _I64, _P, _P, _P, _P, _P, _P]),
     "k2w8_gemm_i8_acc": (ctypes.c_int, [_P, ctypes.POINTER(GemmCfg), _I64, _P, _P, _P]),
     "k2w8_gemm_set_workspace": (ctypes.c_int, [_P, _P, _I64]),
+    "k2w8_gemm_choose": (ctypes.c_int, [ctypes.c_int32, _I64, ctypes.POINTER(GemmCfg), _I64, _I64,
+                                        ctypes.POINTER(GemmChoice)]),
     "k2w8_linear_norm_i8": (
         ctypes.c_int,
         [_P, ctypes.POINTER(PrepareNormCfg), ctypes.POINTER(GemmCfg), _I64, _P, _P, _P, _P, _P, _P,

@@ -26,6 +26,7 @@ import torch
 from ._lib import (
     AttentionCfg,
     GemmCfg,
+    GemmChoice,
     InvalidArgument,
     PrepareGatedCfg,
     PrepareNormCfg,
@@ -439,6 +440,32 @@ class Quantized:
         )
         check(lib().k2w8_quantized_forward(_stream(stream), ctypes.byref(cfg), rows, *args))
         return out
+
+
+_EPILOGUES = {"plain": 0, "resid": 1, "swiglu": 2, "bias": 3, "acc": 4}
+_KERNELS = {0: "few-token", 1: "tile", 2: "tile+tail", 3: "split-k"}
+
+
+def gemm_choose(m, *, cfg: GemmConfig, epilogue="plain", cus=256, workspace_bytes=None) -> dict:
+    """Which kernel the GEMM entry points run for ``m`` tokens with ``cfg`` on a device of
+    ``cus`` compute units (no launch): ``kernel`` (few-token, tile, tile+tail, split-k),
+    the workgroup ``tile`` (m, n), its LDS ``stages``, ``n_big`` (tile+tail) and
+    ``splits`` / ``split_steps`` (split-k). ``workspace_bytes`` defaults to the
+    library's own per-stream workspace."""
+    if workspace_bytes is None:
+        workspace_bytes = int(lib().k2w8_gemm_workspace_bytes())
+    out = GemmChoice()
+    k = cfg.c()
+    check(lib().k2w8_gemm_choose(_EPILOGUES[epilogue], m, ctypes.byref(k), cus, workspace_bytes,
+                                 ctypes.byref(out)))
+    res = {"kernel": _KERNELS[out.kernel]}
+    if out.kernel:
+        res.update(tile=(out.tile_m, out.tile_n), stages=out.stages)
+    if out.kernel == 2:
+        res["n_big"] = out.n_big
+    if out.kernel == 3:
+        res.update(splits=out.splits, split_steps=out.split_steps)
+    return res
 
 
 def probe_mfma_i8(out, *, blocks, iters, random=True, seed=1, stream=None):

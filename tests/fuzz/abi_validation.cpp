@@ -90,6 +90,7 @@ hipError_t splitk_register(hipStream_t, void *, size_t) { return hipSuccess; }
 size_t splitk_workspace_bytes() { return 64u << 20; }
 Workspace splitk_static_scratch(hipError_t *e) { *e = hipSuccess; return Workspace{(void *)0x100000, 16u << 20}; }
 void splitk_install(Workspace) {}
+bool gemm_streams(int, const GemmLaunch &l, int64_t) { return l.m <= 32; }
 }  // namespace k2w8
 
 int main() {
@@ -156,6 +157,28 @@ int main() {
       }
     }
   }
+  // The kernel choice (k2w8_gemm_choose): plan_tiles and the split rule on any
+  // accepted shape, CU count and workspace size.
+  long chosen = 0;
+  for (int it = 0; it < 200000; ++it) {
+    k2w8_gemm_cfg g{128 * (1 + (int64_t)(rng() % 512)), 128 * (1 + (int64_t)(rng() % 256)), 0, 4, 0};
+    g.k_stride = g.k_size;
+    if (rng() % 8 == 0) g.k_size = pick();
+    const int64_t m = rng() % 8 ? 1 + (int64_t)(rng() % (1 << 24)) : pick();
+    const int64_t cus = rng() % 8 ? 1 + (int64_t)(rng() % 4096) : pick();
+    const int64_t ws = rng() % 8 ? (int64_t)(rng() % (1ll << 36)) : pick();
+    k2w8_gemm_choice out;
+    if (k2w8_gemm_choose((int32_t)(rng() % 6) - 1 + 1, m, &g, cus, ws, &out) == K2W8_OK) {
+      ++chosen;
+      REQ(out.kernel >= 0 && out.kernel <= 3);
+      if (out.kernel > 0) REQ(out.tile_m >= 64 && out.tile_n >= 64 && out.stages >= 2);
+      if (out.kernel == 2) REQ(out.n_big > 0 && out.n_big < g.n_size && out.n_big % 256 == 0);
+      if (out.kernel == 3) REQ(out.splits >= 2 && out.split_steps >= 1 && (int64_t)out.splits * out.split_steps * 128 >= g.k_size &&
+                               2 * m * g.n_size * 4 <= ws);
+    }
+  }
+  printf("choices %ld, ", chosen);
+
   // The block entry points (k2w8_block.cpp), which chain the stage calls above and
   // the attention step's, over edge, huge and mostly-valid block shapes and indices.
   const int64_t bedge[] = {-1, 0, 1, 15, 16, 128, 255, 256, 384, 512, 1024, 3072, 6144, 9216, 12288, 15360,

@@ -1,0 +1,96 @@
+"""Which kernel each BASELINE shape runs (k2w8_gemm_choose, the rule launch_gemm
+applies), on the CPU. The expected choices are the kernels the GPU kernel traces show
+for these shapes (profiles/gemm_i8_mid_m_counters.md for config 5,
+profiles/block_linears_4544_kernel_trace.md for the block, the QKV and north-star
+traces), so a change of the rule that moves a measured shape to another kernel shows
+up here."""
+
+import os
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIBDIR = os.path.join(ROOT, "krea2-hrx_amd")
+
+
+@pytest.fixture(scope="module")
+def k2():
+    if not os.path.exists(os.path.join(LIBDIR, "libkrea2_w8a8.so")):
+        subprocess.run(["make", "-s", "-C", LIBDIR], check=True)
+    import krea2_w8a8
+
+    return krea2_w8a8
+
+
+CASES = [
+    # (what, m, k, n, epilogue, expected)
+    ("configs[1] QKV", 4096, 3072, 9216, "plain", {"kernel": "tile", "tile": (256, 192), "stages": 2}),
+    ("north star", 4096, 3072, 12288, "plain", {"kernel": "tile", "tile": (256, 256), "stages": 2}),
+    ("configs[0] bias", 4096, 3072, 3072, "bias", {"kernel": "tile", "tile": (256, 192), "stages": 2}),
+    ("block qkvg", 4544, 3072, 9216, "plain", {"kernel": "tile", "tile": (256, 256), "stages": 2}),
+    ("block wo", 4544, 3072, 3072, "resid", {"kernel": "tile", "tile": (256, 256), "stages": 2}),
+    ("block gate|up", 4544, 3072, 24576, "swiglu", {"kernel": "tile", "tile": (256, 256), "stages": 2}),
+    ("block down", 4544, 12288, 3072, "resid", {"kernel": "tile", "tile": (256, 256), "stages": 2}),
+    ("config 5 QKV, 1 token", 1, 2560, 4096, "plain", {"kernel": "few-token"}),
+    ("config 5 QKV, 77", 77, 2560, 4096, "plain", {"kernel": "few-token"}),
+    ("config 5 up, 77", 77, 2560, 19456, "swiglu", {"kernel": "tile", "tile": (128, 64), "stages": 3}),
+    ("config 5 down, 77", 77, 9728, 2560, "resid",
+     {"kernel": "split-k", "tile": (128, 128), "stages": 3, "splits": 11, "split_steps": 7}),
+    ("config 5 QKV, 256", 256, 2560, 4096, "plain", {"kernel": "tile", "tile": (64, 64), "stages": 4}),
+    ("config 5 up, 256", 256, 2560, 19456, "swiglu", {"kernel": "tile", "tile": (256, 128), "stages": 3}),
+    ("config 5 down, 256", 256, 9728, 2560, "resid",
+     {"kernel": "split-k", "tile": (128, 128), "stages": 3, "splits": 6, "split_steps": 13}),
+    ("config 5 QKV, 512", 512, 2560, 4096, "plain", {"kernel": "tile", "tile": (128, 64), "stages": 3}),
+    ("config 5 up, 512", 512, 2560, 19456, "swiglu", {"kernel": "tile", "tile": (256, 256), "stages": 2}),
+    ("config 5 down, 512", 512, 9728, 2560, "resid",
+     {"kernel": "split-k", "tile": (128, 128), "stages": 3, "splits": 3, "split_steps": 26}),
+    ("a mostly idle last round", 2000, 256, 9216, "plain",
+     {"kernel": "tile+tail", "tile": (256, 256), "stages": 2, "n_big": 8192}),
+]
+
+
+@pytest.mark.parametrize("what,m,k,n,epilogue,expected", CASES, ids=[c[0] for c in CASES])
+def test_baseline_shapes_run_the_measured_kernels(k2, what, m, k, n, epilogue, expected):
+    got = k2.gemm_choose(m, cfg=k2.GemmConfig(k_size=k, n_size=n, k_stride=k), epilogue=epilogue)
+    assert got == expected
+
+
+def test_split_k_needs_room_for_two_slices(k2):
+    cfg = k2.GemmConfig(k_size=9728, n_size=2560, k_stride=9728)
+    # the M=256 down projection splits in the library's workspace and in the 16 MiB
+    # static scratch of the allocation-free entry point, not in 1 MiB
+    assert k2.gemm_choose(256, cfg=cfg, epilogue="resid")["kernel"] == "split-k"
+    assert k2.gemm_choose(256, cfg=cfg, epilogue="resid", workspace_bytes=16 << 20)["kernel"] == "split-k"
+    no_room = k2.gemm_choose(256, cfg=cfg, epilogue="resid", workspace_bytes=1 << 20)
+    assert no_room == {"kernel": "tile", "tile": (64, 64), "stages": 4}
+
+
+def test_every_split_fits_the_static_scratch_on_256_cus(k2):
+    # The allocation-free entry point's promise: on 256 CUs, two int32 slices of every
+    # shape the split rule picks fit its 16 MiB.
+    for m in range(33, 2049, 7):
+        for n in range(128, 32769, 640):
+            for k in (1024, 4224, 9728, 16384, 65536):
+                got = k2.gemm_choose(m, cfg=k2.GemmConfig(k_size=k, n_size=n, k_stride=k), epilogue="plain",
+                                     workspace_bytes=1 << 40)
+                if got["kernel"] == "split-k":
+                    assert 2 * m * n * 4 <= 16 << 20, (m, n, k)
+
+
+def test_the_choice_depends_on_the_cu_count(k2):
+    cfg = k2.GemmConfig(k_size=3072, n_size=9216, k_stride=3072)
+    assert k2.gemm_choose(4096, cfg=cfg, cus=256)["tile"] == (256, 192)
+    # 304 CUs: 576 256x256 tiles are 1.9 rounds, 768 256x192 ones 2.5
+    assert k2.gemm_choose(4096, cfg=cfg, cus=304)["tile"] == (256, 256)
+
+
+def test_bad_arguments_are_refused(k2):
+    cfg = k2.GemmConfig(k_size=3072, n_size=9216, k_stride=3072)
+    for kwargs in (dict(cus=0), dict(cus=5000), dict(workspace_bytes=-1)):
+        with pytest.raises(k2.InvalidArgument):
+            k2.gemm_choose(4096, cfg=cfg, **kwargs)
+    with pytest.raises(k2.InvalidArgument):
+        k2.gemm_choose(0, cfg=cfg)
+    with pytest.raises(k2.InvalidArgument):
+        k2.gemm_choose(4096, cfg=k2.GemmConfig(k_size=3000, n_size=9216, k_stride=3072))
