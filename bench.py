@@ -245,8 +245,29 @@ def main():
 
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(M, K, N, pitch, args.cpu_seconds)
+    result["gemm_kernel_choice"] = kernel_choices(k2, torch.cuda.get_device_properties(0).multi_processor_count)
 
     print(json.dumps(result), flush=True)
+
+
+def kernel_choices(k2, cus):
+    """The kernel and tile each benchmarked GEMM shape runs on this device
+    (k2w8_gemm_choose: the rule the GEMM entry points apply; no launch)."""
+    shapes = [("configs[1] QKV", 4096, 3072, 9216, "plain"), ("north star", 4096, 3072, 12288, "plain"),
+              ("configs[0]", 4096, 3072, 3072, "bias"), ("configs[2] up", 4608, 3072, 24576, "swiglu"),
+              ("configs[2] down", 4608, 12288, 3072, "resid"), ("configs[3] qkv", 4544, 3072, 9216, "plain"),
+              ("configs[3] wo", 4544, 3072, 3072, "resid"), ("configs[3] up", 4544, 3072, 24576, "swiglu"),
+              ("configs[3] down", 4544, 12288, 3072, "resid")]
+    for m in (1, 16, 77, 256, 512):
+        shapes += [(f"configs[4] qkv M={m}", m, 2560, 4096, "plain"), (f"configs[4] up M={m}", m, 2560, 19456, "swiglu"),
+                   (f"configs[4] down M={m}", m, 9728, 2560, "resid")]
+    out = {"cus": cus}
+    for name, m, k, n, epi in shapes:
+        c = k2.gemm_choose(m, cfg=k2.GemmConfig(k_size=k, n_size=n, k_stride=k2.shape.gemm_pitch(k)),
+                           epilogue=epi, cus=cus)
+        out[name] = c["kernel"] + (f" {c['tile'][0]}x{c['tile'][1]}" if "tile" in c else "") + (
+            f" x{c['splits']} slices" if "splits" in c else "")
+    return out
 
 
 def measured_traffic():

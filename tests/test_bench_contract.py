@@ -33,3 +33,16 @@ def test_cpu_baseline_reports_its_sample_cores_and_single_thread_figure():
     assert single["cores"] == 1 and single["value"] > 0
     # the multi-threaded figure is not below the single-threaded one by much (same code)
     assert out["value"] > 0.5 * single["value"]
+
+
+def test_kernel_choices_name_every_benchmarked_shape():
+    import sys
+    sys.path.insert(0, os.path.join(ROOT, "krea2-hrx_amd"))
+    import krea2_w8a8 as k2
+
+    bench = load_bench()
+    out = bench.kernel_choices(k2, 256)
+    assert out["cus"] == 256 and len(out) == 1 + 9 + 15
+    assert out["configs[1] QKV"] == "tile 256x192"
+    assert out["configs[4] down M=256"] == "split-k 128x128 x6 slices"
+    assert out["configs[4] qkv M=1"] == "few-token"
