@@ -208,10 +208,16 @@ int k2w8_gemm_i8_noalloc(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, cons
  * `workspace_bytes` (the library's own: k2w8_gemm_workspace_bytes()), without launching
  * anything: the rule launch_gemm applies, for tuning reports and host-side tests.
  * `epilogue` is 0 plain, 1 residual, 2 SwiGLU, 3 bias, 4 int32 accumulators.
+ * `workspace_required` nonzero describes a call whose workspace is fixed at
+ * `workspace_bytes` and may not be replaced (gemm_i8_noalloc: its static scratch); a shape
+ * such a call refuses reports kernel -1. The library's per-stream workspace is not
+ * available inside a stream capture unless one was registered (gemm_set_workspace) or
+ * a recording installed it: pass workspace_bytes = 0 to see what a captured call runs.
  */
 typedef struct k2w8_gemm_choice {
   int32_t kernel;  /* 0 few-token kernel, 1 tile kernel, 2 256x256 tiles then the last
-                      columns as 128x128 tiles, 3 split K over 128x128 tiles + reduction */
+                      columns as 128x128 tiles, 3 split K over 128x128 tiles + reduction,
+                      -1 refused (workspace_required, two slices do not fit) */
   int32_t tile_m, tile_n; /* kernels 1-3: the workgroup tile (kernel 2: 256x256) */
   int32_t stages;         /* kernels 1-3: LDS stages of the tile kernel */
   int64_t n_big;          /* kernel 2: the columns that run as 256x256 tiles */
@@ -219,7 +225,7 @@ typedef struct k2w8_gemm_choice {
   int32_t splits;         /* kernel 3: slices */
 } k2w8_gemm_choice;
 int k2w8_gemm_choose(int32_t epilogue, int64_t m, const k2w8_gemm_cfg *cfg, int64_t cus,
-                     int64_t workspace_bytes, k2w8_gemm_choice *out);
+                     int64_t workspace_bytes, int32_t workspace_required, k2w8_gemm_choice *out);
 
 /*
  * linear_norm_i8 / linear_plain_i8: one call for a projection:

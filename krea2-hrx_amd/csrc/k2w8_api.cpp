@@ -448,7 +448,7 @@ int k2w8_gemm_i8_noalloc(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, cons
 }
 
 int k2w8_gemm_choose(int32_t epilogue, int64_t m, const k2w8_gemm_cfg *cfg, int64_t cus,
-                     int64_t workspace_bytes, k2w8_gemm_choice *out) {
+                     int64_t workspace_bytes, int32_t workspace_required, k2w8_gemm_choice *out) {
   const char *stage = "gemm_choose";
   if (!cfg || !out) return fail(K2W8_INVALID_ARGUMENT, "%s: null configuration or output", stage);
   int rc = check_gemm_cfg(stage, cfg);
@@ -477,6 +477,10 @@ int k2w8_gemm_choose(int32_t epilogue, int64_t m, const k2w8_gemm_cfg *cfg, int6
   out->kernel = plan.n_big > 0 ? 2 : 1;
   out->n_big = plan.n_big;
   if (plan.tile == GemmTile::kSplit) {
+    if (workspace_required && k2w8::splitk_refused(l.m, l.n, l.k, cus, (size_t)workspace_bytes)) {
+      out->kernel = -1;  // the entry point refuses the shape with INVALID_ARGUMENT
+      return ok();
+    }
     const int per = k2w8::splitk_steps(l.m, l.n, l.k, cus, (size_t)workspace_bytes);
     if (per > 0) {
       out->kernel = 3;

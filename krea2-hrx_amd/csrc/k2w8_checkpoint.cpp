@@ -319,7 +319,7 @@ struct k2w8_checkpoint {
   const uint8_t *bytes(const Entry &e) const { return data + e.begin; }
 
   // Blocks are numbered from 0 without gaps; a block exists when its first attention
-  // projection does (the rule of file.rs:124-129): the count is the first number
+  // projection does (the rule of src/checkpoint/file.rs:115-119): the count is the first number
   // missing from the checkpoint's `blocks.<n>.attn.wq.weight` names.
   int64_t block_count() const {
     static const std::string head = "blocks.", tail = ".attn.wq.weight";
@@ -330,12 +330,15 @@ struct k2w8_checkpoint {
           n.compare(n.size() - tail.size(), tail.size(), tail) != 0)
         continue;
       const std::string digits = n.substr(head.size(), n.size() - head.size() - tail.size());
-      if (digits.empty() || digits.size() > 9 || digits.find_first_not_of("0123456789") != std::string::npos)
+      // Only the decimal form `{i}` names block i: no sign, no leading zero.
+      if (digits.empty() || digits.size() > 9 || digits.find_first_not_of("0123456789") != std::string::npos ||
+          (digits.size() > 1 && digits[0] == '0'))
         continue;
       present.insert(std::stoll(digits));
     }
+    // The reference counts at most one block per tensor of the file.
     int64_t count = 0;
-    while (present.count(count)) ++count;
+    while (count < (int64_t)entries.size() && present.count(count)) ++count;
     return count;
   }
 };

@@ -809,9 +809,7 @@ hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &l) {
   const Workspace ws = l.workspace ? *l.workspace : splitk_workspace(stream);
   // A caller that passes a fixed workspace and requires it: a shape that would split K
   // but whose two slices do not fit is refused before anything is launched.
-  if (l.workspace_required && splitk_steps(l.m, l.n, l.k, cus, SIZE_MAX) > 0 &&
-      (size_t)(2 * l.m * l.n * 4) > ws.bytes)
-    return hipErrorInvalidValue;
+  if (l.workspace_required && splitk_refused(l.m, l.n, l.k, cus, ws.bytes)) return hipErrorInvalidValue;
   const int per = ws.ptr ? splitk_steps(l.m, l.n, l.k, cus, ws.bytes) : 0;
   if (per > 0) {
     int32_t *parts = static_cast<int32_t *>(ws.ptr);

@@ -92,4 +92,12 @@ inline int splitk_steps(int64_t m, int64_t n, int64_t k, int64_t cus, size_t wor
   return (k_steps + per - 1) / per >= 2 ? (int)per : 0;
 }
 
+// A call whose workspace is fixed and required (the allocation-free entry point): a
+// shape that would split K with an unbounded workspace but whose two slices do not fit
+// the fixed one is refused, rather than run on the slower 64x64 tiles.
+inline bool splitk_refused(int64_t m, int64_t n, int64_t k, int64_t cus, size_t workspace_bytes) {
+  return plan_tiles(m, n, k, cus).tile == GemmTile::kSplit && splitk_steps(m, n, k, cus, SIZE_MAX) > 0 &&
+         (size_t)(2 * m * n * 4) > workspace_bytes;
+}
+
 }  // namespace k2w8

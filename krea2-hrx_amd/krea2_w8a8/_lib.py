@@ -160,7 +160,7 @@ SIGNATURES = {
     "k2w8_gemm_i8_acc": (ctypes.c_int, [_P, ctypes.POINTER(GemmCfg), _I64, _P, _P, _P]),
     "k2w8_gemm_set_workspace": (ctypes.c_int, [_P, _P, _I64]),
     "k2w8_gemm_choose": (ctypes.c_int, [ctypes.c_int32, _I64, ctypes.POINTER(GemmCfg), _I64, _I64,
-                                        ctypes.POINTER(GemmChoice)]),
+                                        ctypes.c_int32, ctypes.POINTER(GemmChoice)]),
     "k2w8_linear_norm_i8": (
         ctypes.c_int,
         [_P, ctypes.POINTER(PrepareNormCfg), ctypes.POINTER(GemmCfg), _I64, _P, _P, _P, _P, _P, _P,

@@ -443,23 +443,29 @@ class Quantized:
 
 
 _EPILOGUES = {"plain": 0, "resid": 1, "swiglu": 2, "bias": 3, "acc": 4}
-_KERNELS = {0: "few-token", 1: "tile", 2: "tile+tail", 3: "split-k"}
+_KERNELS = {-1: "refused", 0: "few-token", 1: "tile", 2: "tile+tail", 3: "split-k"}
 
 
-def gemm_choose(m, *, cfg: GemmConfig, epilogue="plain", cus=256, workspace_bytes=None) -> dict:
+def gemm_choose(m, *, cfg: GemmConfig, epilogue="plain", cus=256, workspace_bytes=None,
+                workspace_required=False) -> dict:
     """Which kernel the GEMM entry points run for ``m`` tokens with ``cfg`` on a device of
-    ``cus`` compute units (no launch): ``kernel`` (few-token, tile, tile+tail, split-k),
-    the workgroup ``tile`` (m, n), its LDS ``stages``, ``n_big`` (tile+tail) and
-    ``splits`` / ``split_steps`` (split-k). ``workspace_bytes`` defaults to the
-    library's own per-stream workspace."""
+    ``cus`` compute units (no launch): ``kernel`` (few-token, tile, tile+tail, split-k,
+    or refused), the workgroup ``tile`` (m, n), its LDS ``stages``, ``n_big``
+    (tile+tail) and ``splits`` / ``split_steps`` (split-k).
+
+    ``workspace_bytes`` defaults to the library's own per-stream workspace, which an
+    eager call has; a call captured into a graph without a registered or installed
+    workspace has none (pass 0 for it). ``workspace_required`` describes a call whose
+    workspace is fixed (``gemm_i8_noalloc``'s static scratch): a shape it refuses is
+    reported as ``refused``."""
     if workspace_bytes is None:
         workspace_bytes = int(lib().k2w8_gemm_workspace_bytes())
     out = GemmChoice()
     k = cfg.c()
     check(lib().k2w8_gemm_choose(_EPILOGUES[epilogue], m, ctypes.byref(k), cus, workspace_bytes,
-                                 ctypes.byref(out)))
+                                 1 if workspace_required else 0, ctypes.byref(out)))
     res = {"kernel": _KERNELS[out.kernel]}
-    if out.kernel:
+    if out.kernel > 0:
         res.update(tile=(out.tile_m, out.tile_n), stages=out.stages)
     if out.kernel == 2:
         res["n_big"] = out.n_big

@@ -168,9 +168,11 @@ int main() {
     const int64_t cus = rng() % 8 ? 1 + (int64_t)(rng() % 4096) : pick();
     const int64_t ws = rng() % 8 ? (int64_t)(rng() % (1ll << 36)) : pick();
     k2w8_gemm_choice out;
-    if (k2w8_gemm_choose((int32_t)(rng() % 6) - 1 + 1, m, &g, cus, ws, &out) == K2W8_OK) {
+    const int32_t required = (int32_t)(rng() % 2);
+    if (k2w8_gemm_choose((int32_t)(rng() % 6) - 1 + 1, m, &g, cus, ws, required, &out) == K2W8_OK) {
       ++chosen;
-      REQ(out.kernel >= 0 && out.kernel <= 3);
+      REQ(out.kernel >= (required ? -1 : 0) && out.kernel <= 3);
+      if (out.kernel == -1) REQ(2 * m * g.n_size * 4 > ws);
       if (out.kernel > 0) REQ(out.tile_m >= 64 && out.tile_n >= 64 && out.stages >= 2);
       if (out.kernel == 2) REQ(out.n_big > 0 && out.n_big < g.n_size && out.n_big % 256 == 0);
       if (out.kernel == 3) REQ(out.splits >= 2 && out.split_steps >= 1 && (int64_t)out.splits * out.split_steps * 128 >= g.k_size &&

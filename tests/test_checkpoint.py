@@ -66,6 +66,20 @@ def test_a_whole_model_save_reads_under_the_transformer_names(tmp_path):
             f.get("model.diffusion_model.first.weight")
 
 
+def test_block_count_takes_only_the_decimal_form_of_each_index(tmp_path):
+    # src/checkpoint/file.rs:115-119 looks up exactly `blocks.{i}.attn.wq.weight` for
+    # i = 0, 1, ...: `blocks.01` is not block 1, and `blocks.+1` / `blocks. 1` are no
+    # blocks at all, so this file holds one block.
+    path = tmp_path / "zeros.safetensors"
+    names = ["blocks.0.attn.wq.weight", "blocks.01.attn.wq.weight", "blocks.+1.attn.wq.weight",
+             "blocks.00.attn.wq.weight"]
+    header = "{" + ",".join(
+        f'"{n}":{{"dtype":"I8","shape":[1],"data_offsets":[{i},{i + 1}]}}' for i, n in enumerate(names)) + "}"
+    write_raw(path, header, bytes(len(names)))
+    with Checkpoint(path) as f:
+        assert f.block_count() == 1
+
+
 def test_names_without_a_shared_wrapper_are_kept(tmp_path):
     path = tmp_path / "mixed.safetensors"
     header = ('{"model.blocks.0.attn.wq.weight":{"dtype":"I8","shape":[1],"data_offsets":[0,1]},'

@@ -78,6 +78,32 @@ def test_every_split_fits_the_static_scratch_on_256_cus(k2):
                     assert 2 * m * n * 4 <= 16 << 20, (m, n, k)
 
 
+def test_the_allocation_free_refusal_is_the_choice_rule(k2):
+    # gemm_i8_noalloc's 16 MiB scratch is fixed: on a device with more CUs the split
+    # rule can pick a shape whose two int32 slices do not fit, and the entry point
+    # refuses it (INVALID_ARGUMENT) instead of running 64x64 tiles. 512 CUs, M=1024,
+    # N=2560, K=9728: 160 128x128 tiles split, and 2 x 1024 x 2560 x 4 = 20 MiB > 16 MiB.
+    cfg = k2.GemmConfig(k_size=9728, n_size=2560, k_stride=9728)
+    fixed = dict(cus=512, workspace_bytes=16 << 20)
+    assert k2.gemm_choose(1024, cfg=cfg, epilogue="resid", **fixed, workspace_required=True) == {"kernel": "refused"}
+    # the same fixed size without the requirement falls back to 64x64 tiles
+    assert k2.gemm_choose(1024, cfg=cfg, epilogue="resid", **fixed)["tile"] == (64, 64)
+    # with room for two slices the required workspace splits as usual
+    roomy = dict(cus=512, workspace_bytes=32 << 20)
+    assert k2.gemm_choose(1024, cfg=cfg, epilogue="resid", **roomy, workspace_required=True)["kernel"] == "split-k"
+    # a shape that does not split is never refused
+    wide = k2.GemmConfig(k_size=3072, n_size=9216, k_stride=3072)
+    assert k2.gemm_choose(4096, cfg=wide, **fixed, workspace_required=True)["kernel"] in ("tile", "tile+tail")
+
+
+def test_a_captured_call_without_a_workspace_runs_64x64_tiles(k2):
+    # Inside a stream capture with no registered or installed workspace the library has
+    # none: the M=256 down projection then runs 64x64 tiles, not split K.
+    cfg = k2.GemmConfig(k_size=9728, n_size=2560, k_stride=9728)
+    assert k2.gemm_choose(256, cfg=cfg, epilogue="resid", workspace_bytes=0) == {
+        "kernel": "tile", "tile": (64, 64), "stages": 4}
+
+
 def test_the_choice_depends_on_the_cu_count(k2):
     cfg = k2.GemmConfig(k_size=3072, n_size=9216, k_stride=3072)
     assert k2.gemm_choose(4096, cfg=cfg, cus=256)["tile"] == (256, 192)
