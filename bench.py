@@ -218,6 +218,7 @@ def main():
             "unit": "TOPS",
             "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
             "traffic": measured_traffic(),
+            "traffic_source": traffic_source(),
             "algorithmic_bytes": gemm_bytes,
         },
     }
@@ -272,12 +273,27 @@ def kernel_choices(k2, cus):
 
 def measured_traffic():
     """HBM bytes per gemm_i8 launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
-    passes (calibrated against a copy kernel), or None if they are absent."""
+    passes (calibrated against a copy kernel), or None if they are absent. The counters
+    cannot be read inside this run (they need rocprofv3 --pmc passes of their own), so
+    the value is the committed profile's, and traffic_source() names it."""
     try:
         with open(TRAFFIC_FILE) as f:
             return json.load(f)["gemm_i8"]["traffic_bytes"]
     except (OSError, KeyError, ValueError):
         return None
+
+
+def traffic_source():
+    """Where roofline.traffic comes from: the profile file, the launch and the build it
+    measured, and that this run did not measure it."""
+    src = {"file": os.path.relpath(TRAFFIC_FILE, ROOT), "measured_in_this_run": False}
+    try:
+        with open(TRAFFIC_FILE) as f:
+            d = json.load(f)
+        src.update(launch=d["gemm_i8"]["launch"], build=d.get("measured_build"), commands=d["commands"])
+    except (OSError, KeyError, ValueError):
+        src["missing"] = True
+    return src
 
 
 def event_timed(torch, fn, steps, warmup):

@@ -46,3 +46,15 @@ def test_kernel_choices_name_every_benchmarked_shape():
     assert out["configs[1] QKV"] == "tile 256x192"
     assert out["configs[4] down M=256"] == "split-k 128x128 x6 slices"
     assert out["configs[4] qkv M=1"] == "few-token"
+
+
+def test_roofline_traffic_names_its_source():
+    # roofline.traffic is read from a committed rocprofv3 profile, not measured in the
+    # run: the bench line says which file, launch and build it comes from.
+    bench = load_bench()
+    src = bench.traffic_source()
+    assert src["measured_in_this_run"] is False
+    assert os.path.exists(os.path.join(ROOT, src["file"])) and src["file"].startswith("profiles/")
+    assert "gemm_kernel<256, 192" in src["launch"] and src["build"]
+    assert all("rocprofv3 --pmc" in c for c in src["commands"])
+    assert bench.measured_traffic() > 0
