@@ -197,7 +197,12 @@ int64_t k2w8_gemm_workspace_bytes(void);
  * (2 * m * n_size * 4 bytes > 16 MiB) is refused with INVALID_ARGUMENT; on a 256-CU
  * MI355X the split rule never picks one (it splits only when the 128x128 tiles cover
  * at most half the CUs, so m * n_size <= 2^21). Every call on a device shares that device's
- * array: calls that overlap on one device (on different streams) race on it.
+ * array. Eager calls that split K are ordered on the device: each one's stream waits
+ * (hipStreamWaitEvent, no host wait) for the previous such call's work, whatever its
+ * stream. Calls recorded into a graph are ordered by the graph; replays of two graphs
+ * that both hold such a call must not overlap (on different streams), or they race on
+ * the array. The first call on a device looks up the array's address there and creates
+ * the ordering event; no call allocates device memory.
  */
 int k2w8_gemm_i8_noalloc(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, const int8_t *a,
                          const int8_t *w, const float *scale, const float *a_scale, void *c);
@@ -236,12 +241,15 @@ int k2w8_gemm_choose(int32_t epilogue, int64_t m, const k2w8_gemm_cfg *cfg, int6
  * GEMM's k_size / k_stride must equal the prepare's width / out_stride, its m is
  * `tokens`), and the outputs are bit-identical to calling them in turn; q and q_scale
  * are written as well. They run as the two launches. With the environment variable
- * K2W8_LINEAR_ONE_LAUNCH=1, the wide-tile shapes (whole rounds of 256x256 or 256x192
- * tiles, width <= 3072) run instead in one persistent launch with a grid-wide barrier
- * between the phases (one workgroup per CU); it gives the same bits but measured
- * slower, so it is not the default. That form needs all of its workgroups resident at
- * once: it must not overlap another one-launch call on the device (concurrent streams),
- * or its barrier waits until a bounded poll gives up and the results are wrong.
+ * K2W8_LINEAR_ONE_LAUNCH=1, the wide-tile shapes (whole rounds of 256x192 tiles, width
+ * <= 3072) run instead in one persistent launch with a grid-wide barrier between the
+ * phases (one workgroup per CU); it gives the same bits but measured slower, so it is
+ * not the default. The barrier's count is the launch's own: the first 256 bytes of the
+ * stream's split-K workspace, cleared by a small kernel launched before it (a capture
+ * with no workspace installed or registered records the two launches instead). Its
+ * wait is bounded (K2W8_FUSED_BARRIER_POLLS polls, default 16384); a workgroup that
+ * gives up (other work holding CUs, e.g. a one-launch call on another stream) prepares
+ * the rows of its own tiles again before each tile, so the output stays exact.
  */
 int k2w8_linear_norm_i8(void *stream, const k2w8_prepare_norm_cfg *cfg, const k2w8_gemm_cfg *gemm,
                         int64_t tokens, const void *h, const float *norm_scale,

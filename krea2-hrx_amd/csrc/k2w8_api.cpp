@@ -36,21 +36,23 @@ int runtime(const char *stage, hipError_t e) {
   return fail(K2W8_RUNTIME, "%s: %s", stage, hipGetErrorString(e));
 }
 
-// Large dynamic LDS must be enabled per kernel once per process (and device).
+// Large dynamic LDS is enabled per kernel, once per device (the first call there).
 int ensure_configured(const char *stage) {
-  static std::once_flag once;
-  static hipError_t status = hipSuccess;
-  static const char *what = "";
-  std::call_once(once, [] {
-    what = "enabling the prepare kernels' LDS";
-    status = k2w8::configure_prepare_lds();
-    if (status == hipSuccess) {
-      what = "enabling the GEMM kernels' LDS";
-      status = k2w8::configure_gemm_lds();
-    }
-  });
-  if (status != hipSuccess)
-    return fail(K2W8_RUNTIME, "%s: %s: %s", stage, what, hipGetErrorString(status));
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static bool done[kMaxDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(K2W8_RUNTIME, "%s: the current device: %s", stage, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(K2W8_RUNTIME, "%s: device %d is past the library's %d", stage, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(mu);
+  if (done[dev]) return K2W8_OK;
+  if ((e = k2w8::configure_prepare_lds()) != hipSuccess)
+    return fail(K2W8_RUNTIME, "%s: enabling the prepare kernels' LDS: %s", stage, hipGetErrorString(e));
+  if ((e = k2w8::configure_gemm_lds()) != hipSuccess)
+    return fail(K2W8_RUNTIME, "%s: enabling the GEMM kernels' LDS: %s", stage, hipGetErrorString(e));
+  done[dev] = true;
   return K2W8_OK;
 }
 
@@ -442,9 +444,27 @@ int k2w8_gemm_i8_noalloc(void *stream, const k2w8_gemm_cfg *cfg, int64_t m, cons
   if (rc != K2W8_OK) return rc;
   hipError_t e = hipSuccess;
   const k2w8::Workspace scratch = k2w8::splitk_static_scratch(&e);
-  if (e != hipSuccess) return runtime("gemm_i8_noalloc: the static scratch's device address", e);
-  return run_gemm(stage, k2w8::kEpiPlain, stream, cfg, m, a, w, scale, a_scale, c, nullptr,
-                  nullptr, &scratch);
+  if (e != hipSuccess) return runtime("gemm_i8_noalloc: the static scratch's set-up", e);
+  // Only a split-K launch touches the scratch: those calls are ordered on the device.
+  const int64_t cus = k2w8::device_cus();
+  k2w8::GemmLaunch l;
+  l.m = m;
+  l.n = cfg->n_size;
+  l.k = cfg->k_size;
+  const bool splits = !k2w8::gemm_streams(k2w8::kEpiPlain, l, cus) &&
+                      k2w8::plan_tiles(l.m, l.n, l.k, cus).tile == k2w8::GemmTile::kSplit &&
+                      k2w8::splitk_steps(l.m, l.n, l.k, cus, scratch.bytes) > 0;
+  if (!splits)
+    return run_gemm(stage, k2w8::kEpiPlain, stream, cfg, m, a, w, scale, a_scale, c, nullptr, nullptr,
+                    &scratch);
+  rc = K2W8_OK;
+  e = k2w8::splitk_static_ordered(static_cast<hipStream_t>(stream), [&]() {
+    rc = run_gemm(stage, k2w8::kEpiPlain, stream, cfg, m, a, w, scale, a_scale, c, nullptr, nullptr, &scratch);
+    return hipSuccess;
+  });
+  if (rc != K2W8_OK) return rc;
+  if (e != hipSuccess) return runtime("gemm_i8_noalloc: ordering the static scratch's users", e);
+  return ok();
 }
 
 int k2w8_gemm_choose(int32_t epilogue, int64_t m, const k2w8_gemm_cfg *cfg, int64_t cus,

@@ -2,6 +2,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <functional>
 #include <stdint.h>
 
 namespace k2w8 {
@@ -108,5 +110,11 @@ void splitk_install(Workspace ws);
 // device. Its address on the current device is looked up once per device; `err`
 // receives the lookup's failure.
 Workspace splitk_static_scratch(hipError_t *err);
+// Orders the eager calls that use the current device's static scratch: `stream` waits
+// (on the device, not the host) for the previous such call's work, `launch` enqueues
+// this call's, and its end becomes the next call's wait. Inside a stream capture it
+// only runs `launch`: the graph orders its own calls, and replays of graphs that use
+// the scratch must not overlap one another.
+hipError_t splitk_static_ordered(hipStream_t stream, const std::function<hipError_t()> &launch);
 
 }  // namespace k2w8

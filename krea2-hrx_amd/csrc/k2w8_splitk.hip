@@ -153,13 +153,18 @@ thread_local Workspace t_installed;
 // allocates. 16 MiB holds at least two K slices of every shape the split-K rule picks
 // (it splits only when 128x128 tiles cover at most half of the 256 CUs: m x n <= 2^21
 // outputs, 8 MiB of int32 per slice). Every call on a device shares that device's copy;
-// calls that overlap on one device race on it. Each slice overwrites its whole part, so
-// nothing needs clearing between calls.
+// eager calls are ordered on the device (splitk_static_ordered), captured ones by their
+// graph. Each slice overwrites its whole part, so nothing needs clearing between calls.
 constexpr size_t kScratchBytes = size_t(16) << 20;
 static __device__ __align__(256) int32_t scratch[kScratchBytes / sizeof(int32_t)];
 
 namespace splitk {
-std::map<int, void *> g_scratch;  // device -> the address of that device's `scratch`
+struct Scratch {
+  void *ptr = nullptr;         // the address of that device's `scratch`
+  hipEvent_t last = nullptr;   // the end of the last eager call that used it
+};
+std::map<int, Scratch> g_scratch;  // device -> its scratch
+std::mutex g_order;                // held across one call's wait, launches and record
 }  // namespace splitk
 
 Workspace splitk_static_scratch(hipError_t *err) {
@@ -168,13 +173,34 @@ Workspace splitk_static_scratch(hipError_t *err) {
   if ((*err = hipGetDevice(&dev)) != hipSuccess) return Workspace{};
   std::lock_guard<std::mutex> guard(splitk::g_lock);
   const auto it = splitk::g_scratch.find(dev);
-  if (it != splitk::g_scratch.end()) return Workspace{it->second, kScratchBytes};
+  if (it != splitk::g_scratch.end()) return Workspace{it->second.ptr, kScratchBytes};
   // The array's name is a host-side stand-in; the device copy's address comes from the
-  // runtime, once per device, with that device current.
-  void *p = nullptr;
-  if ((*err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess) return Workspace{};
-  splitk::g_scratch[dev] = p;
-  return Workspace{p, kScratchBytes};
+  // runtime, once per device, with that device current. The ordering event is made in
+  // the same set-up step.
+  splitk::Scratch sc;
+  if ((*err = hipGetSymbolAddress(&sc.ptr, HIP_SYMBOL(scratch))) != hipSuccess) return Workspace{};
+  if ((*err = hipEventCreateWithFlags(&sc.last, hipEventDisableTiming)) != hipSuccess) return Workspace{};
+  splitk::g_scratch[dev] = sc;
+  return Workspace{sc.ptr, kScratchBytes};
+}
+
+hipError_t splitk_static_ordered(hipStream_t stream, const std::function<hipError_t()> &launch) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  hipEvent_t last = nullptr;
+  {
+    std::lock_guard<std::mutex> guard(splitk::g_lock);
+    const auto it = splitk::g_scratch.find(dev);
+    if (it != splitk::g_scratch.end()) last = it->second.last;
+  }
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  if ((e = hipStreamIsCapturing(stream, &capture)) != hipSuccess) return e;
+  if (!last || capture != hipStreamCaptureStatusNone) return launch();
+  std::lock_guard<std::mutex> order(splitk::g_order);
+  if ((e = hipStreamWaitEvent(stream, last, 0)) != hipSuccess) return e;
+  if ((e = launch()) != hipSuccess) return e;
+  return hipEventRecord(last, stream);
 }
 
 size_t splitk_workspace_bytes() { return splitk::kWorkspaceBytes; }

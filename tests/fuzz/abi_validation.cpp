@@ -20,6 +20,13 @@ static long g_gemm = 0, g_prep = 0, g_other = 0, g_bad = 0;
 #define REQ(c) do { if (!(c)) { fprintf(stderr, "violated: %s (line %d)\n", #c, __LINE__); ++g_bad; } } while (0)
 static bool al(const void *p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
+// No GPU here: the entry points' per-device set-up sees device 0 (this definition
+// takes the place of the HIP runtime's for the code linked into this program).
+extern "C" hipError_t hipGetDevice(int *device) {
+  *device = 0;
+  return hipSuccess;
+}
+
 namespace k2w8 {
 hipError_t configure_gemm_lds() { return hipSuccess; }
 hipError_t configure_prepare_lds() { return hipSuccess; }
@@ -89,6 +96,7 @@ hipError_t launch_attention(hipStream_t, const AttentionLaunch &l) {
 hipError_t splitk_register(hipStream_t, void *, size_t) { return hipSuccess; }
 size_t splitk_workspace_bytes() { return 64u << 20; }
 Workspace splitk_static_scratch(hipError_t *e) { *e = hipSuccess; return Workspace{(void *)0x100000, 16u << 20}; }
+hipError_t splitk_static_ordered(hipStream_t, const std::function<hipError_t()> &launch) { return launch(); }
 void splitk_install(Workspace) {}
 bool gemm_streams(int, const GemmLaunch &l, int64_t) { return l.m <= 32; }
 }  // namespace k2w8

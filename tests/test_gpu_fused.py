@@ -1,9 +1,11 @@
 """The fused prepare -> GEMM entry points (k2w8_linear_norm_i8, k2w8_linear_plain_i8):
 bit-identical to the two entry points called in turn (q, q_scale and the output), in
-the one-launch form (K2W8_LINEAR_ONE_LAUNCH=1: whole rounds of 256x256 or 256x192
-tiles in one persistent kernel) and in the default two-launch form; the one-launch
-kernel's grid barrier leaves its counters at zero, so back-to-back calls and graph
-replays give the same results."""
+the one-launch form (K2W8_LINEAR_ONE_LAUNCH=1: whole rounds of 256x192 tiles in one
+persistent kernel) and in the default two-launch form. The one-launch kernel's grid
+barrier count is the launch's own (cleared before each launch, kept in the stream's
+workspace), so back-to-back calls, graph replays and calls on two streams at once give
+the same results; and a barrier that gives up (forced from the host by a poll bound of
+0) still gives exact output, every kernel exiting normally."""
 
 import os
 
@@ -58,9 +60,10 @@ def run(c, fused, out=None, q=None, s=None):
 
 
 SHAPES = [
-    ("plain", 4096, 3072, 12288),  # north star: 768 tiles of 256x256, one launch
+    ("plain", 4096, 3072, 12288),  # north star: 1024 tiles of 256x192, one launch
     ("norm", 4096, 3072, 9216),    # configs[1]: 768 tiles of 256x192, one launch
-    ("norm", 2048, 2048, 8192),    # 256 tiles of 256x256 (one round), width 2048
+    ("norm", 2048, 2048, 12288),   # 512 tiles of 256x192, width 2048 (two runs per lane)
+    ("norm", 2048, 2048, 8192),    # not whole 256x192 columns: the two-launch fallback
     ("norm", 4544, 3072, 9216),    # ragged rounds: the two-launch fallback
     ("plain", 300, 1024, 1024),    # mid-M: the two-launch fallback
 ]
@@ -181,3 +184,59 @@ def test_block_pairs_equal_their_two_entry_points(pair, m, k, n):
     (q1, s1, o1), (q2, s2, o2) = res
     assert torch.equal(q1, q2) and torch.equal(s1, s2)
     assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+
+
+@pytest.mark.parametrize("kind,m,k,n", [("norm", 4096, 3072, 9216), ("plain", 2048, 2048, 12288)])
+def test_a_barrier_that_gives_up_still_gives_exact_output(kind, m, k, n, monkeypatch):
+    # A poll bound of 0: every workgroup gives up at the barrier at once and prepares
+    # the rows of each of its tiles itself. The output must equal the two launches',
+    # and a following call with the default bound must too (its count starts at 0).
+    c = case(kind, m, k, n, seed=11 + m)
+    q2, s2, o2 = run(c, fused=False)
+    monkeypatch.setenv("K2W8_LINEAR_ONE_LAUNCH", "1")
+    monkeypatch.setenv("K2W8_FUSED_BARRIER_POLLS", "0")
+    q1, s1, o1 = run(c, fused=True)
+    torch.cuda.synchronize()
+    assert torch.equal(q1, q2) and torch.equal(s1, s2)
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+    monkeypatch.delenv("K2W8_FUSED_BARRIER_POLLS")
+    q3, s3, o3 = run(c, fused=True)
+    torch.cuda.synchronize()
+    assert torch.equal(q3, q2) and torch.equal(o3.view(torch.int16), o2.view(torch.int16))
+
+
+def test_one_launch_calls_on_two_streams_at_once(monkeypatch):
+    # Two host threads, each calling the one-launch form on its own stream several
+    # times: the launches overlap on the device, each counts its own arrivals, and
+    # every output equals the two launches' (ctypes releases the GIL during a call).
+    import threading
+
+    monkeypatch.setenv("K2W8_LINEAR_ONE_LAUNCH", "1")
+    cases = [case("norm", 4096, 3072, 9216, seed=21), case("plain", 4096, 3072, 12288, seed=22)]
+    wants = []
+    for c in cases:
+        _, _, o = run(c, fused=False)
+        wants.append(o)
+    torch.cuda.synchronize()
+    outs = [[torch.zeros_like(w) for _ in range(4)] for w in wants]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    errors = []
+
+    def worker(i):
+        try:
+            with torch.cuda.stream(streams[i]):
+                for o in outs[i]:
+                    run(cases[i], fused=True, out=o)
+        except Exception as e:  # noqa: BLE001 - reported by the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    for i, w in enumerate(wants):
+        for j, o in enumerate(outs[i]):
+            assert torch.equal(o.view(torch.int16), w.view(torch.int16)), (i, j)

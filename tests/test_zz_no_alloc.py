@@ -2,7 +2,8 @@
 bit-identical to k2w8_gemm_i8 on two calls in a row (the second smaller, both splitting
 K into the static scratch) and on a shape that does not split; and no device memory
 allocated by a call on a stream the library has never seen (where k2w8_gemm_i8 would
-allocate its 64 MiB per-stream workspace)."""
+allocate its 64 MiB per-stream workspace); and eager calls on two streams at once,
+which share the scratch, stay exact (the library orders them on the device)."""
 
 import ctypes
 
@@ -66,3 +67,41 @@ def test_no_alloc_gemm_allocates_nothing_on_a_new_stream():
     free1, _ = torch.cuda.mem_get_info()
     assert free0 - free1 < (8 << 20), (free0, free1)  # a per-stream workspace is 64 MiB
     assert np.array_equal(host(got), host(want))
+
+
+def test_no_alloc_calls_on_two_streams_at_once():
+    # Two host threads enqueue split-K calls on their own streams with no ordering of
+    # their own: the library makes each wait for the previous user of the scratch.
+    import threading
+
+    rng = np.random.default_rng(73)
+    shapes = [(256, 9728, 2560), (200, 9728, 2560)]
+    ops = [operands(rng, m, k, n) for m, k, n in shapes]
+    wants = []
+    for (m, k, n), o in zip(shapes, ops):
+        want = torch.zeros((m, n), dtype=torch.float16, device="cuda")
+        call("k2w8_gemm_i8", torch.cuda.current_stream(), m, k, n, o, want)
+        wants.append(want)
+    torch.cuda.synchronize()
+    outs = [[torch.zeros_like(w) for _ in range(6)] for w in wants]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    errors = []
+
+    def worker(i):
+        try:
+            m, k, n = shapes[i]
+            for o in outs[i]:
+                call("k2w8_gemm_i8_noalloc", streams[i], m, k, n, ops[i], o)
+        except Exception as e:  # noqa: BLE001 - reported by the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    for i, w in enumerate(wants):
+        for j, o in enumerate(outs[i]):
+            assert np.array_equal(host(o), host(w)), (i, j)
