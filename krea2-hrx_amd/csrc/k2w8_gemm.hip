@@ -16,6 +16,7 @@
 // kernels/gemm_i8_swiglu_256.loom:569-660.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "k2w8_gemm_common.hpp"
 #include "k2w8_gemm_plan.hpp"
@@ -400,7 +401,11 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs &g, int split, v16
 // group 0's through LDS (integer addition, exact) and group 0 runs the epilogue. On a
 // small tile (64x64 with one workgroup per CU) that gives each SIMD a second wave, so
 // the MFMAs of one overlap the transfer issue of the other.
-template <int BM, int BN, int WM, int WN, int BK, int STAGES, int EPI, int KG = 1>
+//
+// kBackward: the workgroups of odd rounds (one workgroup per CU, 32 CUs per XCD) step
+// through their K steps last to first, so they start on what the XCD's L2 still holds
+// of the previous round's last steps. The int32 sums do not depend on the order.
+template <int BM, int BN, int WM, int WN, int BK, int STAGES, int EPI, int KG = 1, bool kBackward = false>
 __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int bid, uint8_t *smem) {
   constexpr int kCw = WM * WN;      // waves of one K group
   constexpr int kWaves = kCw * KG;  // waves of the workgroup
@@ -469,9 +474,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int bid, uint8_t *s
   const uint32_t a_lds = lds0 + vw0 * kAIns * 1024;
   const uint32_t b_lds = lds0 + BM * BK + vw0 * kBIns * 1024;
 
+  const bool backward = kBackward && (((bid / kXcds) / kCusPerXcd) & 1);
   auto issue = [&](int kt) {
     if (!producer) return;
-    const uint32_t so = (uint32_t)((kt % STAGES) * kStage), ko = (uint32_t)(kt * BK);
+    const int step = backward ? kt_count - 1 - kt : kt;
+    const uint32_t so = (uint32_t)((kt % STAGES) * kStage), ko = (uint32_t)(step * BK);
 #pragma unroll
     for (int j = 0; j < kPer; ++j)
 #pragma unroll
@@ -644,6 +651,13 @@ __global__ __launch_bounds__(WM *WN *KG * 64) void gemm_kernel(GemmArgs g) {
   gemm_tile<BM, BN, WM, WN, BK, STAGES, EPI, KG>(g, blockIdx.x, smem);
 }
 
+// The same tile with odd rounds stepping through K backwards (gemm_tile's kBackward).
+template <int BM, int BN, int WM, int WN, int BK, int STAGES, int EPI>
+__global__ __launch_bounds__(WM *WN * 64) void gemm_kernel_backward(GemmArgs g) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  gemm_tile<BM, BN, WM, WN, BK, STAGES, EPI, 1, true>(g, blockIdx.x, smem);
+}
+
 template <int BM, int BN, int WM, int WN, int BK, int STAGES, int KG = 1>
 struct TileConfig {
   static constexpr int kThreads = WM * WN * KG * 64;
@@ -676,6 +690,45 @@ hipError_t launch_tile(int epi, hipStream_t stream, const GemmArgs &a) {
       break;
   }
   return hipGetLastError();
+}
+
+// The backward-K form of a wide tile (plain, residual, SwiGLU and bias epilogues).
+template <int BM, int BN, int WM, int WN, int BK, int STAGES>
+hipError_t launch_tile_backward(int epi, hipStream_t stream, const GemmArgs &a) {
+  using T = TileConfig<BM, BN, WM, WN, BK, STAGES>;
+  const int tiles = ((a.m + BM - 1) / BM) * (a.n / BN);
+  dim3 grid(tiles), block(T::kThreads);
+  switch (epi) {
+    case kEpiPlain:
+      hipLaunchKernelGGL((gemm_kernel_backward<BM, BN, WM, WN, BK, STAGES, kEpiPlain>), grid, block, T::kLds, stream, a);
+      break;
+    case kEpiResid:
+      hipLaunchKernelGGL((gemm_kernel_backward<BM, BN, WM, WN, BK, STAGES, kEpiResid>), grid, block, T::kLds, stream, a);
+      break;
+    case kEpiSwiglu:
+      hipLaunchKernelGGL((gemm_kernel_backward<BM, BN, WM, WN, BK, STAGES, kEpiSwiglu>), grid, block, T::kLds, stream, a);
+      break;
+    case kEpiBias:
+      hipLaunchKernelGGL((gemm_kernel_backward<BM, BN, WM, WN, BK, STAGES, kEpiBias>), grid, block, T::kLds, stream, a);
+      break;
+    default:
+      return launch_tile<BM, BN, WM, WN, BK, STAGES>(epi, stream, a);
+  }
+  return hipGetLastError();
+}
+
+template <int BM, int BN, int WM, int WN, int BK, int STAGES>
+hipError_t set_lds_tile_backward() {
+  using T = TileConfig<BM, BN, WM, WN, BK, STAGES>;
+  const void *fns[4] = {reinterpret_cast<const void *>(gemm_kernel_backward<BM, BN, WM, WN, BK, STAGES, kEpiPlain>),
+                        reinterpret_cast<const void *>(gemm_kernel_backward<BM, BN, WM, WN, BK, STAGES, kEpiResid>),
+                        reinterpret_cast<const void *>(gemm_kernel_backward<BM, BN, WM, WN, BK, STAGES, kEpiSwiglu>),
+                        reinterpret_cast<const void *>(gemm_kernel_backward<BM, BN, WM, WN, BK, STAGES, kEpiBias>)};
+  for (const void *f : fns) {
+    hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)T::kLds);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 template <int BM, int BN, int WM, int WN, int BK, int STAGES, int KG = 1>
@@ -754,6 +807,8 @@ hipError_t launch_splitk_reduce(int epilogue, hipStream_t stream, const int32_t 
 hipError_t configure_gemm_lds() {
   hipError_t e = gemm::set_lds_tile<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>();
   if (e == hipSuccess) e = gemm::set_lds_tile<256, 192, 4, 2, 128, 2>();
+  if (e == hipSuccess) e = gemm::set_lds_tile_backward<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>();
+  if (e == hipSuccess) e = gemm::set_lds_tile_backward<256, 192, 4, 2, 128, 2>();
   if (e == hipSuccess) e = gemm::set_lds_tile<256, 128, kMidWm, kMidWn, 128, 2>();
   if (e == hipSuccess) e = gemm::set_lds_tile<128, 128, 2, 2, 128, kS128Stages>();
   if (e == hipSuccess) e = gemm::set_lds_tile<64, 64, 2, 2, 128, kS64Stages, kS64Kg>();
@@ -774,14 +829,23 @@ hipError_t launch_gemm(int epilogue, hipStream_t stream, const GemmLaunch &l) {
   if (gemm_streams(epilogue, l, cus)) return launch_skinny(epilogue, stream, l);
   gemm::GemmArgs a = gemm::args_of(l, epilogue);
   const TilePlan plan = plan_tiles(l.m, l.n, l.k, cus);
+  // K2W8_GEMM_BACKWARD=1 (read on every call): the wide tiles' odd rounds step through
+  // K backwards (gemm_tile's kBackward); the same bits, fewer L2 misses by the model.
+  const char *bw = getenv("K2W8_GEMM_BACKWARD");
+  const bool backward = bw && bw[0] == '1';
   switch (plan.tile) {
     case GemmTile::k256x192:
+      if (backward) return gemm::launch_tile_backward<256, 192, 4, 2, 128, 2>(epilogue, stream, a);
       return gemm::launch_tile<256, 192, 4, 2, 128, 2>(epilogue, stream, a);
     case GemmTile::k256x256: {
+      if (plan.n_big == 0 && backward)
+        return gemm::launch_tile_backward<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>(epilogue, stream, a);
       if (plan.n_big == 0) return gemm::launch_tile<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>(epilogue, stream, a);
       gemm::GemmArgs big = a, tail = a;
       big.n = (int)plan.n_big;
-      hipError_t e = gemm::launch_tile<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>(epilogue, stream, big);
+      hipError_t e = backward
+                         ? gemm::launch_tile_backward<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>(epilogue, stream, big)
+                         : gemm::launch_tile<256, 256, kBigWm, kBigWn, kBigBk, kBigStages>(epilogue, stream, big);
       if (e != hipSuccess) return e;
       tail.n = (int)(l.n - plan.n_big);
       tail.w = a.w + plan.n_big * l.lda;

@@ -13,6 +13,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int kXcds = 8;  // MI355X: 8 XCDs, workgroups dispatched round-robin
+constexpr int kCusPerXcd = 32;  // MI355X: 256 CUs
 
 struct GemmArgs {
   const int8_t *a, *w;

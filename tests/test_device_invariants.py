@@ -66,7 +66,11 @@ def _gemm_tiles():
     for k, args, blocks in _kernels("gemm_kernel"):
         bm, bn, wm, wn, bk, stages, epi, kg = args
         tiles.append((k[".name"], pm.Tile(bm, bn, wm, wn, bk, stages, epi, kg), blocks))
-    assert len(tiles) >= 40, "the tile kernels the build instantiates"
+    # the backward-K forms (one K group): the same LDS schedule, other global offsets
+    for k, args, blocks in _kernels("gemm_kernel_backward"):
+        bm, bn, wm, wn, bk, stages, epi = args
+        tiles.append((k[".name"], pm.Tile(bm, bn, wm, wn, bk, stages, epi), blocks))
+    assert len(tiles) >= 48, "the tile kernels the build instantiates"
     return tiles
 
 
