@@ -194,8 +194,9 @@ hipError_t splitk_static_ordered(hipStream_t stream, const std::function<hipErro
     const auto it = splitk::g_scratch.find(dev);
     if (it != splitk::g_scratch.end()) last = it->second.last;
   }
+  // (the null stream, torch's default one, is never capturing)
   hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-  if ((e = hipStreamIsCapturing(stream, &capture)) != hipSuccess) return e;
+  if (stream && (e = hipStreamIsCapturing(stream, &capture)) != hipSuccess) return e;
   if (!last || capture != hipStreamCaptureStatusNone) return launch();
   std::lock_guard<std::mutex> order(splitk::g_order);
   if ((e = hipStreamWaitEvent(stream, last, 0)) != hipSuccess) return e;
