@@ -52,6 +52,8 @@ int ensure_configured(const char *stage) {
     return fail(K2W8_RUNTIME, "%s: enabling the prepare kernels' LDS: %s", stage, hipGetErrorString(e));
   if ((e = k2w8::configure_gemm_lds()) != hipSuccess)
     return fail(K2W8_RUNTIME, "%s: enabling the GEMM kernels' LDS: %s", stage, hipGetErrorString(e));
+  if ((e = k2w8::configure_fused_lds()) != hipSuccess)
+    return fail(K2W8_RUNTIME, "%s: enabling the one-launch kernels' LDS: %s", stage, hipGetErrorString(e));
   done[dev] = true;
   return K2W8_OK;
 }

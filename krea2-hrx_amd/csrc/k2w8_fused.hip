@@ -27,8 +27,6 @@
 
 #include <stdlib.h>
 
-#include <mutex>
-
 namespace k2w8 {
 
 namespace fused {
@@ -111,15 +109,8 @@ size_t lds_bytes(int width) {
   return stage_lds > factor_lds ? stage_lds : factor_lds;
 }
 
-// The kernels' LDS limit, raised once per device (every launch's need is at most the
-// widest row's, K = 3072).
-hipError_t configure(int dev) {
-  static std::mutex mu;
-  constexpr int kMaxDevices = 64;
-  static bool done[kMaxDevices] = {};
-  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
-  std::lock_guard<std::mutex> lock(mu);
-  if (done[dev]) return hipSuccess;
+// The kernels' LDS limit (every launch's need is at most the widest row's, K = 3072).
+hipError_t configure() {
   const struct {
     const void *fn;
     size_t lds;
@@ -133,7 +124,6 @@ hipError_t configure(int dev) {
     const hipError_t e = hipFuncSetAttribute(k.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)k.lds);
     if (e != hipSuccess) return e;
   }
-  done[dev] = true;
   return hipSuccess;
 }
 
@@ -159,6 +149,8 @@ hipError_t launch(hipStream_t stream, const PrepareArgs &p, const gemm::GemmArgs
 
 }  // namespace fused
 
+hipError_t configure_fused_lds() { return fused::configure(); }
+
 // The fused launch for whole rounds of 256x192 tiles (the tile choice of launch_gemm
 // for QKV-like shapes); hipErrorNotSupported for every other shape, and for a stream
 // without a workspace (a capture with none installed or registered), which the caller
@@ -175,10 +167,6 @@ hipError_t launch_prepare_gemm(int kind, hipStream_t stream, int64_t tokens,
   if (t192 % cus != 0) return hipErrorNotSupported;
   const Workspace ws = gl.workspace ? *gl.workspace : splitk_workspace(stream);
   if (!ws.ptr || ws.bytes < fused::kStateBytes) return hipErrorNotSupported;
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e == hipSuccess) e = fused::configure(dev);
-  if (e != hipSuccess) return e;
   PrepareArgs p;
   p.h = static_cast<const uint16_t *>(pl.h);
   p.gate = nullptr;

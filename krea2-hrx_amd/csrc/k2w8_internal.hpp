@@ -61,6 +61,8 @@ bool skinny_streams(int epilogue, const GemmLaunch &g, int64_t cus);
 bool gemm_streams(int epilogue, const GemmLaunch &g, int64_t cus);
 hipError_t launch_skinny(int epilogue, hipStream_t stream, const GemmLaunch &g);
 hipError_t configure_gemm_lds();
+// The one-launch prepare -> GEMM kernels' LDS limit, on the current device.
+hipError_t configure_fused_lds();
 hipError_t configure_skinny_lds();
 
 // bf16 <-> f16 transport: direction 1 bf16 -> f16, 2 f16 -> bf16.

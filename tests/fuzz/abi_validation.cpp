@@ -30,6 +30,7 @@ extern "C" hipError_t hipGetDevice(int *device) {
 namespace k2w8 {
 hipError_t configure_gemm_lds() { return hipSuccess; }
 hipError_t configure_prepare_lds() { return hipSuccess; }
+hipError_t configure_fused_lds() { return hipSuccess; }
 int device_cus() { return 256; }
 hipError_t prepare_gated_ready(hipStream_t) { return hipSuccess; }
 hipError_t launch_gemm(int epi, hipStream_t, const GemmLaunch &l) {
