@@ -8,7 +8,9 @@ tests can hold invariants of the device code that no host-side run exercises.
 from __future__ import annotations
 
 import functools
+import hashlib
 import os
+import re
 import struct
 import subprocess
 import tempfile
@@ -78,3 +80,15 @@ def disassembly(image_index: int, path: str = LIB) -> dict[str, list[str]]:
         elif cur is not None and line.strip():
             funcs[cur].append(line.strip())
     return funcs
+
+
+def fingerprints(path: str = LIB) -> dict[str, str]:
+    """A hash of each function's instructions (the disassembly without addresses and
+    encodings), by symbol name: equal hashes mean the same machine code, wherever the
+    linker placed it."""
+    out = {}
+    for n in range(len(code_objects(path))):
+        for name, lines in disassembly(n, path).items():
+            text = "\n".join(re.sub(r"\s*//.*", "", line).strip() for line in lines)
+            out[name] = hashlib.sha256(text.encode()).hexdigest()[:16]
+    return out
