@@ -43,6 +43,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="headline step only")
+    p.add_argument("--backward-k", action="store_true",
+                   help="also time the north star with odd rounds stepping through K backwards "
+                        "(K2W8_GEMM_BACKWARD=1, an opt-in variant)")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--probe", choices=["north_star", "skinny", "attention", "mfma_peak"],
                    help="run one workload a few times and exit (a short program for "
@@ -406,10 +409,13 @@ def north_star(k2, torch, weights, hidden, args):
     os.environ["K2W8_LINEAR_ONE_LAUNCH"] = "1"
     sec_f = event_timed(torch, one_launch, args.steps, args.warmup)
     os.environ["K2W8_LINEAR_ONE_LAUNCH"] = "0"
-    # Odd rounds stepping through K backwards (same bits; fewer L2 misses by the model).
-    os.environ["K2W8_GEMM_BACKWARD"] = "1"
-    sec_b = event_timed(torch, gemm, args.steps, args.warmup)
-    os.environ["K2W8_GEMM_BACKWARD"] = "0"
+    # Odd rounds stepping through K backwards (same bits; fewer L2 misses by the model),
+    # on request only: an opt-in variant.
+    sec_b = None
+    if args.backward_k:
+        os.environ["K2W8_GEMM_BACKWARD"] = "1"
+        sec_b = event_timed(torch, gemm, args.steps, args.warmup)
+        os.environ["K2W8_GEMM_BACKWARD"] = "0"
     ops = 2.0 * M * N * K
     tops = ops / sec / 1e12
     return {"M": M, "K": K, "N": N, "us": round(sec * 1e6, 2), "TOPS": round(tops, 1),
@@ -422,7 +428,7 @@ def north_star(k2, torch, weights, hidden, args):
             "us_prepare_plus_gemm": round(sec_c * 1e6, 2),
             "pct_of_int8_peak_prepare_plus_gemm": round(100 * ops / sec_c / 1e12 / PEAK_INT8_TOPS, 2),
             "us_prepare_gemm_one_launch": round(sec_f * 1e6, 2),
-            "us_backward_k_odd_rounds": round(sec_b * 1e6, 2),
+            "us_backward_k_odd_rounds": round(sec_b * 1e6, 2) if sec_b is not None else None,
             "timing": "HIP events on the launch stream around each call, mean"}
 
 
