@@ -220,6 +220,7 @@ def test_one_launch_calls_on_two_streams_at_once(monkeypatch):
     torch.cuda.synchronize()
     outs = [[torch.zeros_like(w) for _ in range(4)] for w in wants]
     streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()  # the outputs' fills (default stream) before the workers' streams
     errors = []
 
     def worker(i):

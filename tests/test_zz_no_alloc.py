@@ -85,6 +85,7 @@ def test_no_alloc_calls_on_two_streams_at_once():
     torch.cuda.synchronize()
     outs = [[torch.zeros_like(w) for _ in range(6)] for w in wants]
     streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()  # the outputs' fills (default stream) before the workers' streams
     errors = []
 
     def worker(i):
