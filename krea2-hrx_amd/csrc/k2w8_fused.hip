@@ -161,10 +161,7 @@ hipError_t configure_fused_lds() { return fused::configure(); }
 hipError_t launch_prepare_gemm(int kind, hipStream_t stream, int64_t tokens,
                                const PrepareLaunch &pl, const GemmLaunch &gl) {
   const int cus = device_cus();
-  if (pl.width > 3072 || gl.m != tokens || gl.n % 192 != 0 || gl.lda != pl.out_stride)
-    return hipErrorNotSupported;
-  const int64_t t192 = ((gl.m + 255) / 256) * (gl.n / 192);
-  if (t192 % cus != 0) return hipErrorNotSupported;
+  if (!one_launch_fits(tokens, gl.m, gl.n, pl.width, gl.lda, pl.out_stride, cus)) return hipErrorNotSupported;
   const Workspace ws = gl.workspace ? *gl.workspace : splitk_workspace(stream);
   if (!ws.ptr || ws.bytes < fused::kStateBytes) return hipErrorNotSupported;
   PrepareArgs p;

@@ -100,4 +100,13 @@ inline bool splitk_refused(int64_t m, int64_t n, int64_t k, int64_t cus, size_t 
          (size_t)(2 * m * n * 4) > workspace_bytes;
 }
 
+// Whether a prepare -> GEMM pair can run as the one persistent launch (one workgroup
+// per CU, all resident): whole rounds of 256x192 tiles, rows the prepare writes at the
+// stride the GEMM reads, and a row of at most 3072 (the prepare phase's registers).
+inline bool one_launch_fits(int64_t tokens, int64_t m, int64_t n, int64_t width, int64_t lda,
+                            int64_t out_stride, int64_t cus) {
+  if (width > 3072 || m != tokens || lda != out_stride || n % 192 != 0 || cus < 1) return false;
+  return ((m + 255) / 256) * (n / 192) % cus == 0;
+}
+
 }  // namespace k2w8

@@ -120,3 +120,17 @@ def test_bad_arguments_are_refused(k2):
         k2.gemm_choose(0, cfg=cfg)
     with pytest.raises(k2.InvalidArgument):
         k2.gemm_choose(4096, cfg=k2.GemmConfig(k_size=3000, n_size=9216, k_stride=3072))
+
+
+def test_the_one_launch_rule_admits_whole_rounds_of_256x192_tiles(tmp_path):
+    # k2w8_linear_{norm,plain}_i8's one-launch form (K2W8_LINEAR_ONE_LAUNCH=1) runs only
+    # where every workgroup is resident with one per CU: whole rounds of 256x192 tiles.
+    import shutil
+    if shutil.which("g++") is None:
+        pytest.skip("needs g++")
+    exe = tmp_path / "one_launch_rule"
+    src = os.path.join(ROOT, "tests", "fuzz", "one_launch_rule.cpp")
+    subprocess.run(["g++", "-O1", "-std=c++17", f"-I{LIBDIR}/csrc", src, "-o", str(exe)], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert int(r.stdout.split()[-1]) > 0
